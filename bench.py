@@ -1,0 +1,191 @@
+"""Benchmark: ms per request of the decision-model forward on one MI355X.
+
+A step is one request of the workload through the HIP path: the encoder + decision head + scorer
+forward on the GPU (s1_forward, inputs uploaded by the call) and the answer decode on the CPU.
+The headline workload is a 512-token state with 10 questions on the ModernBERT-large shape
+(10 rows of ~555-590 tokens, one padded batch), with synthetic seeded bf16 weights.
+
+Printed: one JSON line with the metric, `roofline` for the dominant kernel (algorithmic FLOPs per
+launch / the kernel's mean duration, from HIP events recorded on the model's stream around each
+launch during the timed steps), and `cpu_baseline` (the oracle, numpy f32, on a bounded sample
+of the same workload on this host's cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ms/request (128 & 512 tok, 1 & 10 questions); GEMM MFMA util %"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+BASELINE_M5_10Q512_MS = 379.0  # sys1rust on an Apple M5, README.md:111
+
+
+def gemm_flops(name: str, T: int, P: int, R: int, d: int, I: int, S: int) -> float:
+    """Algorithmic FLOPs of one launch of each GEMM kernel (2 M N K)."""
+    table = {
+        "wqkv_rope": 2.0 * T * d * 3 * d,
+        "wqkv": 2.0 * T * d * 3 * d,
+        "wo": 2.0 * T * d * d,
+        "wi_geglu": 2.0 * T * d * 2 * I,
+        "wi": 2.0 * T * d * 2 * I,
+        "wo2": 2.0 * T * I * d,
+        "head_in_proj": 2.0 * T * d * 3 * d,
+    }
+    return table.get(name, 0.0)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="state512_10q")
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload the CPU baseline runs")
+    ap.add_argument("--settings", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by request with no collective, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from sys1rust_amd.backend import HipBackend, synth_checkpoint
+    from sys1rust_amd.decode import decode_answers
+    from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, SCORER_WIDTH, workload
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    enc_json, agent_json = json.dumps(MODERNBERT_LARGE), json.dumps(AGENT)
+    t0 = time.time()
+    ckpt = synth_checkpoint(enc_json, agent_json, seed=args.seed, scorer_width=SCORER_WIDTH)
+    settings = ",".join(x for x in ["ops", args.settings] if x)
+    model = HipBackend(ckpt, enc_json, agent_json, settings=settings)
+    model.warmup()
+    print(f"[bench] model ready in {time.time() - t0:.1f}s: {model.name()} {model.active_kernels()}",
+          file=sys.stderr, flush=True)
+
+    def run(b, steps, warmup):
+        for _ in range(warmup):
+            out = model.forward(b)
+            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype)
+        model.op_stats_reset()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            out = model.forward(b)
+            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) * 1e3 / steps, model.op_stats()
+
+    # Context shapes (1 question at 128 and 512 tokens), then the headline workload last so its
+    # per-kernel statistics are the ones reported.
+    shapes = {}
+    for name in ["state128_1q", "state512_1q"]:
+        b = workload(name, seed=args.seed)
+        ms, _ = run(b, max(5, args.steps // 2), args.warmup)
+        shapes[name] = round(ms, 4)
+        print(f"[bench] {name}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
+    b = workload(args.workload, seed=args.seed)
+    ms, stats = run(b, args.steps, args.warmup)
+    shapes[args.workload] = round(ms, 4)
+    print(f"[bench] {args.workload}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
+
+    T = b.total_tokens()
+    d, I = MODERNBERT_LARGE["hidden_size"], MODERNBERT_LARGE["intermediate_size"]
+    P, R = b.n * (1 + b.kmax), b.n * b.kmax
+    kernels = {}
+    for name, (count, tot) in stats.items():
+        avg = tot / max(count, 1)
+        f = gemm_flops(name, T, P, R, d, I, SCORER_WIDTH)
+        kernels[name] = {"launches": count, "avg_us": round(avg * 1e3, 3), "total_ms_per_step": round(tot / args.steps, 4)}
+        if f:
+            tf = f / (avg * 1e-3) / 1e12
+            kernels[name]["tflops"] = round(tf, 1)
+            kernels[name]["mfma_util"] = round(tf / PEAK_BF16_TFLOPS, 4)
+    gemms = {k: v for k, v in kernels.items() if "tflops" in v}
+    dom = max(gemms, key=lambda k: gemms[k]["total_ms_per_step"])
+    dk = gemms[dom]
+    gemm_flop_step = sum(gemm_flops(k, T, P, R, d, I, SCORER_WIDTH) * v["launches"] / args.steps for k, v in gemms.items())
+    gemm_ms_step = sum(v["total_ms_per_step"] for v in gemms.values())
+    roofline = {
+        "kernel": dom,
+        "bound": "mfma",
+        "achieved": dk["tflops"],
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(dk["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "traffic": None,
+        "flop_per_launch": gemm_flops(dom, T, P, R, d, I, SCORER_WIDTH),
+        "avg_launch_us": dk["avg_us"],
+        "all_encoder_gemms_tflops": round(gemm_flop_step / (gemm_ms_step * 1e-3) / 1e12, 1),
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle.oracle import Oracle
+
+        try:
+            from threadpoolctl import threadpool_info
+
+            threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        except Exception:
+            threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+        o = Oracle(ckpt, MODERNBERT_LARGE, AGENT)
+        rows = list(range(min(args.cpu_rows, b.n)))
+        sub = b.rows(rows)
+        o.forward(sub)  # warm caches
+        t = time.perf_counter()
+        lg, _ = o.forward(sub)
+        decode_answers(lg, sub.kmax, sub.marker_count, sub.qtype)
+        per_row = (time.perf_counter() - t) * 1e3 / len(rows)
+        cpu = {
+            "value": round(per_row * b.n, 1),
+            "unit": "ms/request",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"{len(rows)} of the {b.n} rows of one {args.workload} request through the numpy f32 oracle "
+                      f"(encoder, head, scorer, decode), scaled by {b.n}; rows are independent",
+        }
+        print(f"[bench] cpu baseline {cpu['value']} ms/request on {threads} threads", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms/request",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(ms / BASELINE_M5_10Q512_MS, 5),
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: encoder+head+scorer forward and answer decode, ModernBERT-large "
+                               f"shape, random-init bf16 weights",
+                   "rows": b.n, "tokens": T, "padded_len": b.len, "seed": args.seed},
+        "sequences_per_s": round(b.n / (ms * 1e-3), 1),
+        "shapes_ms_per_request": shapes,
+        "gemm_mfma_util": {k: v["mfma_util"] for k, v in gemms.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

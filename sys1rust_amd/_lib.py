@@ -1,0 +1,113 @@
+"""ctypes binding of libsys1hip.so (include/sys1hip.h).
+
+The library is loaded from this package directory only, and a missing library is an error: there
+is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsys1hip.so"
+
+S1_OK, S1_ERR_CONFIG, S1_ERR_WEIGHTS, S1_ERR_BACKEND, S1_ERR_BATCH = 0, 1, 2, 3, 4
+ERR_NAMES = {1: "Config", 2: "Weights", 3: "Backend", 4: "Batch"}
+
+
+class S1Error(RuntimeError):
+    """A nonzero return of the C ABI: `.kind` is one of ERR_NAMES' values."""
+
+    def __init__(self, code: int, msg: str):
+        self.code = code
+        self.kind = ERR_NAMES.get(code, str(code))
+        super().__init__(f"{self.kind}: {msg}")
+
+
+_lib = None
+
+u32p = C.POINTER(C.c_uint32)
+u64p = C.POINTER(C.c_uint64)
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int32)
+
+# name -> (restype, argtypes); every symbol declared in include/sys1hip.h
+SIGNATURES = {
+    "s1_model_create": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
+    "s1_model_create_from_bytes": (
+        C.c_int,
+        [C.c_void_p, C.c_size_t, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(C.c_void_p)],
+    ),
+    "s1_forward": (
+        C.c_int,
+        [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, u32p, u32p, u64p, u32p, u64p, u32p, f32p, f32p],
+    ),
+    "s1_encoder_hidden": (
+        C.c_int,
+        [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, u32p, u32p, u64p, u32p, u64p, u32p, f32p],
+    ),
+    "s1_padded_len": (C.c_size_t, [C.c_void_p, C.c_size_t, C.c_size_t]),
+    "s1_name": (C.c_char_p, [C.c_void_p]),
+    "s1_active_kernels": (C.c_char_p, [C.c_void_p]),
+    "s1_warmup": (C.c_int, [C.c_void_p]),
+    "s1_last_error": (C.c_char_p, []),
+    "s1_model_destroy": (None, [C.c_void_p]),
+    "s1_synth_checkpoint": (
+        C.c_int,
+        [C.c_char_p, C.c_char_p, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)],
+    ),
+    "s1_pack_tables": (
+        C.c_int,
+        [C.c_uint32, C.c_uint32, C.c_uint32, u32p, u64p, u32p, u64p, i32p, i32p, i32p, i32p, u32p],
+    ),
+    "s1_op_stats": (
+        C.c_int,
+        [C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.c_int],
+    ),
+    "s1_op_stats_reset": (None, [C.c_void_p]),
+    "s1k_gemm": (
+        C.c_int,
+        [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+         C.c_int, C.c_int, C.c_void_p],
+    ),
+    "s1k_qkv_rope": (
+        C.c_int,
+        [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p,
+         C.c_void_p],
+    ),
+    "s1k_split_rope": (
+        C.c_int,
+        [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+    ),
+    "s1k_attention": (
+        C.c_int,
+        [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, i32p, C.c_int, C.c_int, C.c_float, C.c_void_p,
+         C.c_void_p],
+    ),
+    "s1k_layernorm": (
+        C.c_int,
+        [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_int, C.c_void_p, C.c_void_p],
+    ),
+}
+
+
+def lib() -> C.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m sys1rust_amd.build` "
+                "(there is no fallback path)"
+            )
+        l = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != S1_OK:
+        raise S1Error(rc, lib().s1_last_error().decode(errors="replace"))

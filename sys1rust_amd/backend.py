@@ -1,0 +1,135 @@
+"""HipBackend: laya_core's `Backend` trait (runtime/crates/laya-core/src/backend.rs:109-133)
+over the C ABI of libsys1hip, for the harness and tests.
+
+Same names, argument meaning and errors as the trait: `name`, `forward(batch)`,
+`active_kernels`, `padded_len(len, rows)`, `warmup`, `encoder_hidden(batch)`. Errors surface as
+`S1Error` with the kind (Config / Weights / Backend / Batch) of laya_core::Error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+from . import _lib
+from ._lib import S1Error, check, f32p, u32p, u64p
+from .workloads import Batch
+
+
+@dataclass
+class BackendOutput:
+    """backend.rs:100-107: `n * kmax` logits (-1e4 where the marker mask is false) and the
+    `n * hidden` pooled head output at position 0."""
+
+    logits: np.ndarray
+    pooled: np.ndarray
+
+
+def synth_checkpoint(encoder_config: str, agent_config: str | None, seed: int, scorer_width: int = 1024,
+                     n_act: int = 2, jitter: bool = True) -> bytes:
+    """Seeded synthetic decision-model checkpoint (safetensors bytes, reference tensor names)."""
+    L = _lib.lib()
+    n = C.c_size_t(0)
+    enc = encoder_config.encode()
+    ag = agent_config.encode() if agent_config else None
+    check(L.s1_synth_checkpoint(enc, ag, seed, scorer_width, n_act, int(jitter), None, 0, C.byref(n)))
+    buf = C.create_string_buffer(n.value)
+    check(L.s1_synth_checkpoint(enc, ag, seed, scorer_width, n_act, int(jitter), buf, n.value, C.byref(n)))
+    return buf.raw[: n.value]
+
+
+def _ptr(a: np.ndarray, ty):
+    return a.ctypes.data_as(ty)
+
+
+def _batch_arrays(b: Batch):
+    ids = np.ascontiguousarray(b.input_ids, dtype=np.uint32)
+    am = np.ascontiguousarray(b.attention_mask, dtype=np.uint32)
+    sl = np.ascontiguousarray(b.seq_lens, dtype=np.uint64)
+    mp = np.ascontiguousarray(b.marker_pos, dtype=np.uint32)
+    if mp.size == 0:
+        mp = np.zeros(1, dtype=np.uint32)
+    mc = np.ascontiguousarray(b.marker_count, dtype=np.uint64)
+    qt = np.ascontiguousarray(b.qtype, dtype=np.uint32)
+    return ids, am, sl, mp, mc, qt
+
+
+class HipBackend:
+    """One loaded model on one GPU (MlxBackend's role, runtime/crates/laya-mlx/src/lib.rs:1803-1879)."""
+
+    def __init__(self, weights, encoder_config: str, agent_config: str | None = None, settings: str = "",
+                 device: int = 0):
+        L = _lib.lib()
+        out = C.c_void_p()
+        enc = encoder_config.encode()
+        ag = agent_config.encode() if agent_config else None
+        st = settings.encode()
+        if isinstance(weights, (bytes, bytearray)):
+            buf = (C.c_char * len(weights)).from_buffer_copy(weights) if isinstance(weights, bytes) else \
+                (C.c_char * len(weights)).from_buffer(weights)
+            rc = L.s1_model_create_from_bytes(buf, len(weights), enc, ag, st, device, C.byref(out))
+        else:
+            rc = L.s1_model_create(str(Path(weights)).encode(), enc, ag, st, device, C.byref(out))
+        check(rc)
+        self._h = out
+        self.d = int(__import__("json").loads(encoder_config)["hidden_size"])
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.lib().s1_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def name(self) -> str:
+        return _lib.lib().s1_name(self._h).decode()
+
+    def active_kernels(self) -> list:
+        s = _lib.lib().s1_active_kernels(self._h).decode()
+        return [k for k in s.split(",") if k]
+
+    def padded_len(self, length: int, rows: int) -> int:
+        return int(_lib.lib().s1_padded_len(self._h, length, rows))
+
+    def warmup(self) -> None:
+        check(_lib.lib().s1_warmup(self._h))
+
+    def forward(self, b: Batch) -> BackendOutput:
+        ids, am, sl, mp, mc, qt = _batch_arrays(b)
+        logits = np.zeros(max(b.n * b.kmax, 1), dtype=np.float32)
+        pooled = np.zeros(max(b.n * self.d, 1), dtype=np.float32)
+        check(_lib.lib().s1_forward(self._h, b.n, b.len, b.kmax, _ptr(ids, u32p), _ptr(am, u32p), _ptr(sl, u64p),
+                                    _ptr(mp, u32p), _ptr(mc, u64p), _ptr(qt, u32p), _ptr(logits, f32p),
+                                    _ptr(pooled, f32p)))
+        return BackendOutput(logits[: b.n * b.kmax], pooled[: b.n * self.d])
+
+    def encoder_hidden(self, b: Batch) -> np.ndarray:
+        ids, am, sl, mp, mc, qt = _batch_arrays(b)
+        hidden = np.zeros(max(b.n * b.len * self.d, 1), dtype=np.float32)
+        check(_lib.lib().s1_encoder_hidden(self._h, b.n, b.len, b.kmax, _ptr(ids, u32p), _ptr(am, u32p),
+                                           _ptr(sl, u64p), _ptr(mp, u32p), _ptr(mc, u64p), _ptr(qt, u32p),
+                                           _ptr(hidden, f32p)))
+        return hidden[: b.n * b.len * self.d]
+
+    def op_stats(self) -> dict:
+        """Per-kernel {name: (launches, total_ms)} since the last reset (`ops` setting)."""
+        L = _lib.lib()
+        cap = 256
+        names = C.create_string_buffer(1 << 16)
+        counts = (C.c_uint64 * cap)()
+        tot = (C.c_double * cap)()
+        k = L.s1_op_stats(self._h, names, len(names), counts, tot, cap)
+        ns = names.value.decode().split("\n")
+        return {ns[i]: (int(counts[i]), float(tot[i])) for i in range(k)}
+
+    def op_stats_reset(self) -> None:
+        _lib.lib().s1_op_stats_reset(self._h)
+
+
+__all__ = ["HipBackend", "BackendOutput", "S1Error", "synth_checkpoint"]

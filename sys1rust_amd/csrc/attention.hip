@@ -1,0 +1,204 @@
+// Fused attention for gfx950: softmax(q k^T * scale + mask) v over packed variable-length rows,
+// one pass over the keys with an online softmax (f32 statistics), both products on MFMA.
+//
+// Replaces MLX's scaled_dot_product_attention on the encoder's global layers (pad mask only,
+// runtime/crates/laya-mlx/src/lib.rs:1653-1656), its local layers (pad + |i - j| <= 64 window,
+// lib.rs:1399-1417, 1644-1649; the banded form 1600-1622) and the decision head's attention
+// (lib.rs:1710-1712). The reference's additive -1e4 masks give every masked key an exp() of
+// exactly 0 in f32 for any query that has one visible key, which every real token has (itself),
+// so a hard mask over the row's own keys computes the same values; padding never enters the
+// packed layout at all.
+//
+// Work split: a workgroup of 4 wavefronts takes up to 128 queries of one sequence and one head;
+// each wave owns 32 queries. Keys stream through LDS in chunks of 64 (K as [key][dim], V
+// transposed as [dim][key]); waves skip chunks outside their window.
+//
+// The products are computed transposed so that every softmax statistic lives in one lane:
+//   S^T[key, q] = K . Q^T   (A = K rows from LDS, B = the wave's Q held in registers)
+// lane l then holds query l % 32 and keys 8g + 4h + r (h = l / 32), so the row max and sum are a
+// lane-local reduction plus one exchange with lane l ^ 32.
+//   O^T[dim, q] += V^T . P^T
+// reuses P^T straight from the S^T accumulators: within a 16-key MFMA step, operand slot
+// 8h + j stands for key 16s + 8(j / 4) + 4h + (j % 4), and the V^T operand is read from LDS with
+// the same key order (two 8-byte reads), so no shuffle of P is needed.
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace s1 {
+
+namespace {
+
+constexpr int KC = 64;       // keys per chunk
+constexpr int LDS_W = 72;    // padded LDS row (bf16 elements)
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+template <bool LOCAL>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[KC * LDS_W];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[64 * LDS_W];
+
+  const AttnTile tl = a.tiles[blockIdx.x];
+  const int head = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5;       // lane half
+  const int col = lane & 31;      // query column within the wave
+
+  const uint16_t* __restrict__ Qh = a.q + size_t(head) * a.Tq * 64;
+  const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.Tk * 64;
+  const uint16_t* __restrict__ Vh = a.v + size_t(head) * a.Tk * 64;
+
+  const int wq0 = tl.q0 + wave * 32;
+  const bool wave_active = wq0 < tl.q1;
+  const int qi = wq0 + col;
+  const bool qvalid = qi < tl.q1;
+  const int qld = min(qi, tl.q1 - 1);
+  const int qk = a.qkey ? a.qkey[qld] : qld;  // key-buffer index of this query
+
+  // Key range of the workgroup and of this wave.
+  int kb0 = tl.k0, kb1 = tl.k1;
+  int wk0 = tl.k0, wk1 = tl.k1;
+  if constexpr (LOCAL) {
+    const int first = a.qkey ? a.qkey[tl.q0] : tl.q0;
+    const int last = a.qkey ? a.qkey[tl.q1 - 1] : tl.q1 - 1;
+    kb0 = max(tl.k0, first - a.window);
+    kb1 = min(tl.k1, last + a.window + 1);
+    if (wave_active) {
+      const int wf = a.qkey ? a.qkey[wq0] : wq0;
+      const int wlq = min(wq0 + 31, tl.q1 - 1);
+      const int wl = a.qkey ? a.qkey[wlq] : wlq;
+      wk0 = max(tl.k0, wf - a.window);
+      wk1 = min(tl.k1, wl + a.window + 1);
+    }
+  }
+
+  // This lane's slice of its query: dims 16kb + 8h .. +7 for kb = 0..3 (MFMA B operand).
+  bf16x8 qf[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+
+  const float sl2 = a.scale * 1.4426950408889634f;  // fold log2(e): exp(x) = exp2(x log2 e)
+  float m = NEG_INF, l = 0.0f;
+  f32x16 o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+
+  for (int c0 = kb0; c0 < kb1; c0 += KC) {
+    __syncthreads();
+    // Stage 64 keys x 64 dims of K and V (clamped at the range end; those slots are masked).
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int c = tid + it * 256;
+      const int key = c >> 3, dc = (c & 7) * 8;
+      const int kg = min(c0 + key, kb1 - 1);
+      const uint4 kv = *reinterpret_cast<const uint4*>(Kh + size_t(kg) * 64 + dc);
+      *reinterpret_cast<uint4*>(&sK[key * LDS_W + dc]) = kv;
+      const uint4 vv = *reinterpret_cast<const uint4*>(Vh + size_t(kg) * 64 + dc);
+      sVt[(dc + 0) * LDS_W + key] = uint16_t(vv.x);
+      sVt[(dc + 1) * LDS_W + key] = uint16_t(vv.x >> 16);
+      sVt[(dc + 2) * LDS_W + key] = uint16_t(vv.y);
+      sVt[(dc + 3) * LDS_W + key] = uint16_t(vv.y >> 16);
+      sVt[(dc + 4) * LDS_W + key] = uint16_t(vv.z);
+      sVt[(dc + 5) * LDS_W + key] = uint16_t(vv.z >> 16);
+      sVt[(dc + 6) * LDS_W + key] = uint16_t(vv.w);
+      sVt[(dc + 7) * LDS_W + key] = uint16_t(vv.w >> 16);
+    }
+    __syncthreads();
+    if (!wave_active) continue;
+    if constexpr (LOCAL) {
+      if (c0 + KC <= wk0 || c0 >= wk1) continue;
+    }
+
+    // S^T for two 32-key tiles.
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[t][e] = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[(t * 32 + col) * LDS_W + kb * 16 + hl * 8]);
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+      }
+    }
+    // Scale (base-2 logits) and mask.
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = c0 + t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+        bool ok = key < kb1;
+        if constexpr (LOCAL) ok = ok && abs(key - qk) <= a.window;
+        const float v = ok ? s[t][e] * sl2 : NEG_INF;
+        s[t][e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float alpha = (m == NEG_INF) ? 0.0f : exp2f(m - mn);
+    float psum = 0.0f;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = s[t][sb * 8 + j];
+          const float p = (v == NEG_INF) ? 0.0f : exp2f(v - mn);
+          psum += p;
+          pf[t][sb][j] = __bf16(p);
+        }
+    l = l * alpha + psum;
+    m = mn;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+
+    // O^T += V^T . P^T over the 64 keys (4 MFMA k-steps of 16 keys) for both 32-dim halves.
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int kbase = t * 32 + sb * 16 + hl * 4;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const uint16_t* vr = &sVt[(dt * 32 + col) * LDS_W];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
+          const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+        }
+      }
+  }
+
+  if (!wave_active) return;
+  const float lt = l + __shfl_xor(l, 32, 64);
+  if (!qvalid) return;
+  const float inv = 1.0f / lt;
+  uint16_t* orow = a.out + size_t(qi) * a.ldo + head * 64;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dim = dt * 32 + g * 8 + hl * 4;
+      uint2 w;
+      w.x = pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
+      w.y = pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + dim) = w;
+    }
+}
+
+}  // namespace
+
+void attn_launch(const AttnArgs& a, hipStream_t st) {
+  if (a.ntiles <= 0) return;
+  dim3 grid(a.ntiles, a.heads);
+  if (a.window >= 0)
+    hipLaunchKernelGGL(attn_kernel<true>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(attn_kernel<false>, grid, dim3(256), 0, st, a);
+}
+
+}  // namespace s1

@@ -1,0 +1,254 @@
+// Bandwidth-bound kernels of the forward: embedding + LayerNorm, LayerNorm (with or without
+// bias), the qkv split + RoPE pass, GeGLU, row gathers and the scorer's final dot product.
+// Each row is owned by one wavefront (reductions stay in registers and cross-lane shuffles); every
+// global access is a coalesced 16-byte vector per lane.
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace s1 {
+
+namespace {
+
+// Row statistics of a wave-owned row of PL*64 floats held as v[PL] per lane.
+template <int PL>
+__device__ __forceinline__ void ln_stats(const float* v, int d, float eps, float& mean, float& rstd) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) s += v[i];
+  mean = wave_sum(s) / float(d);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const float c = v[i] - mean;
+    q += c * c;
+  }
+  const float var = wave_sum(q) / float(d);
+  rstd = 1.0f / sqrtf(var + eps);
+}
+
+// Lane l owns elements [8l + 512c, 8l + 512c + 8) for c = 0 .. PL/8 - 1.
+template <int PL>
+__global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restrict__ emb, const int* __restrict__ ids,
+                                                      const float* __restrict__ w, float eps, int T, int d,
+                                                      float* __restrict__ h, uint16_t* __restrict__ x) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const uint16_t* src = emb + size_t(ids[row]) * d;
+  float v[PL];
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) {
+    const uint4 u = *reinterpret_cast<const uint4*>(src + c * 512 + lane * 8);
+    unpack8(u, v + c * 8);
+  }
+  float mean, rstd;
+  ln_stats<PL>(v, d, eps, mean, rstd);
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) {
+    const int o = c * 512 + lane * 8;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (v[c * 8 + e] - mean) * rstd * w[o + e];
+    float4* hp = reinterpret_cast<float4*>(h + size_t(row) * d + o);
+    hp[0] = make_float4(y[0], y[1], y[2], y[3]);
+    hp[1] = make_float4(y[4], y[5], y[6], y[7]);
+    *reinterpret_cast<uint4*>(x + size_t(row) * d + o) = pack8(y);
+  }
+}
+
+template <int PL>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, const int* __restrict__ rows,
+                                                       const float* __restrict__ w, const float* __restrict__ b,
+                                                       float eps, int T, int d, uint16_t* __restrict__ yb,
+                                                       float* __restrict__ yf, const float* __restrict__ addv,
+                                                       const int* __restrict__ seg, float* __restrict__ yplus) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const int src_row = rows ? rows[row] : row;
+  const float* src = x + size_t(src_row) * d;
+  float v[PL];
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) {
+    const float4* p = reinterpret_cast<const float4*>(src + c * 512 + lane * 8);
+    const float4 a = p[0], bq = p[1];
+    v[c * 8 + 0] = a.x; v[c * 8 + 1] = a.y; v[c * 8 + 2] = a.z; v[c * 8 + 3] = a.w;
+    v[c * 8 + 4] = bq.x; v[c * 8 + 5] = bq.y; v[c * 8 + 6] = bq.z; v[c * 8 + 7] = bq.w;
+  }
+  float mean, rstd;
+  ln_stats<PL>(v, d, eps, mean, rstd);
+  const float* av = addv ? addv + size_t(seg[row]) * d : nullptr;
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) {
+    const int o = c * 512 + lane * 8;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y[e] = (v[c * 8 + e] - mean) * rstd * w[o + e];
+      if (b) y[e] += b[o + e];
+    }
+    if (yb) *reinterpret_cast<uint4*>(yb + size_t(row) * d + o) = pack8(y);
+    if (yf) {
+      float4* hp = reinterpret_cast<float4*>(yf + size_t(row) * d + o);
+      hp[0] = make_float4(y[0], y[1], y[2], y[3]);
+      hp[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    if (yplus) {
+      float z[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = y[e] + av[o + e];
+      float4* hp = reinterpret_cast<float4*>(yplus + size_t(row) * d + o);
+      hp[0] = make_float4(z[0], z[1], z[2], z[3]);
+      hp[1] = make_float4(z[4], z[5], z[6], z[7]);
+    }
+  }
+}
+
+// One thread per (token, head, quarter of the 32 rotation pairs): pairs i0 .. i0 + 7 with
+// i0 = 8 * quarter, i.e. dims [i0, i0 + 8) and [i0 + 32, i0 + 40) of the head, for q, k and v.
+__global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restrict__ qkv, int T, int d,
+                                                        const int* __restrict__ pos, const float* __restrict__ ct,
+                                                        const float* __restrict__ stab, uint16_t* __restrict__ q,
+                                                        uint16_t* __restrict__ k, uint16_t* __restrict__ v) {
+  const int H = d >> 6;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long long)T * H * 4) return;
+  const int quarter = int(gid & 3);
+  const int head = int((gid >> 2) % H);
+  const int t = int((gid >> 2) / H);
+  const int i0 = quarter * 8;
+  const uint16_t* src = qkv + size_t(t) * 3 * d + head * 64 + i0;
+  const size_t dst = (size_t(head) * T + t) * 64 + i0;
+  float c[8], s[8];
+  const bool rope = ct != nullptr;
+  if (rope) {
+    const int p = pos[t];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      c[j] = ct[p * 32 + i0 + j];
+      s[j] = stab[p * 32 + i0 + j];
+    }
+  }
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const uint16_t* sp = src + part * d;
+    uint16_t* dp = (part == 0 ? q : k) + dst;
+    const uint4 a = *reinterpret_cast<const uint4*>(sp);
+    const uint4 b = *reinterpret_cast<const uint4*>(sp + 32);
+    if (!rope) {
+      *reinterpret_cast<uint4*>(dp) = a;
+      *reinterpret_cast<uint4*>(dp + 32) = b;
+      continue;
+    }
+    float x1[8], x2[8], y1[8], y2[8];
+    unpack8(a, x1);
+    unpack8(b, x2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      y1[j] = x1[j] * c[j] - x2[j] * s[j];
+      y2[j] = x1[j] * s[j] + x2[j] * c[j];
+    }
+    *reinterpret_cast<uint4*>(dp) = pack8(y1);
+    *reinterpret_cast<uint4*>(dp + 32) = pack8(y2);
+  }
+  const uint16_t* sv = src + 2 * d;
+  *reinterpret_cast<uint4*>(v + dst) = *reinterpret_cast<const uint4*>(sv);
+  *reinterpret_cast<uint4*>(v + dst + 32) = *reinterpret_cast<const uint4*>(sv + 32);
+}
+
+__global__ __launch_bounds__(256) void geglu_kernel(const uint16_t* __restrict__ wi, int T, int I,
+                                                   uint16_t* __restrict__ act) {
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int per_row = I / 8;
+  if (gid >= (long long)T * per_row) return;
+  const int t = int(gid / per_row), c = int(gid % per_row) * 8;
+  const uint16_t* r = wi + size_t(t) * 2 * I;
+  float x[8], g[8], y[8];
+  unpack8(*reinterpret_cast<const uint4*>(r + c), x);
+  unpack8(*reinterpret_cast<const uint4*>(r + I + c), g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = gelu_erf(x[e]) * g[e];
+  *reinterpret_cast<uint4*>(act + size_t(t) * I + c) = pack8(y);
+}
+
+__global__ __launch_bounds__(256) void gather_f32_kernel(const float* __restrict__ x, const int* __restrict__ rows,
+                                                        int R, int d, float* __restrict__ out) {
+  const int r = blockIdx.x;
+  if (r >= R) return;
+  const float4* s = reinterpret_cast<const float4*>(x + size_t(rows[r]) * d);
+  float4* o = reinterpret_cast<float4*>(out + size_t(r) * d);
+  for (int i = threadIdx.x; i < d / 4; i += 256) o[i] = s[i];
+}
+
+__global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
+                                                    const float* __restrict__ b, int R, int d, float* __restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  float acc = 0.0f;
+  for (int o = lane * 8; o < d; o += 512) {
+    float v[8];
+    unpack8(*reinterpret_cast<const uint4*>(x + size_t(row) * d + o), v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += v[e] * w[o + e];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) out[row] = acc + (b ? b[0] : 0.0f);
+}
+
+}  // namespace
+
+void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
+                     uint16_t* x_out, hipStream_t st) {
+  if (T <= 0) return;
+  dim3 grid((T + 3) / 4);
+  switch (d) {
+    case 512: hipLaunchKernelGGL(embed_ln_kernel<8>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 1024: hipLaunchKernelGGL(embed_ln_kernel<16>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 2048: hipLaunchKernelGGL(embed_ln_kernel<32>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+  }
+}
+
+void layernorm_launch(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
+                      uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
+                      hipStream_t st) {
+  if (T <= 0) return;
+  dim3 grid((T + 3) / 4);
+  switch (d) {
+    case 512:
+      hipLaunchKernelGGL(layernorm_kernel<8>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+    case 1024:
+      hipLaunchKernelGGL(layernorm_kernel<16>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+    case 2048:
+      hipLaunchKernelGGL(layernorm_kernel<32>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+  }
+}
+
+void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
+                       uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t st) {
+  const long long n = (long long)T * (d / 64) * 4;
+  if (n <= 0) return;
+  hipLaunchKernelGGL(split_rope_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, T, d, pos, cos_t, sin_t,
+                     q, k, v);
+}
+
+void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st) {
+  const long long n = (long long)T * (I / 8);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(geglu_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, wi, T, I, act);
+}
+
+void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out, hipStream_t st) {
+  if (R <= 0) return;
+  hipLaunchKernelGGL(gather_f32_kernel, dim3(R), dim3(256), 0, st, x, rows, R, d, out);
+}
+
+void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st) {
+  if (R <= 0) return;
+  hipLaunchKernelGGL(rowdot_kernel, dim3((R + 3) / 4), dim3(256), 0, st, x, w, b, R, d, out);
+}
+
+}  // namespace s1

@@ -1,0 +1,86 @@
+// Host-side launch interface of the HIP kernels. Every pointer is a device pointer; bf16 data is
+// passed as uint16_t. Launchers enqueue on the given stream and never synchronise.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace s1 {
+
+enum GemmEpi { EPI_BF16 = 0, EPI_RESID = 1, EPI_GEGLU = 2, EPI_F32 = 3, EPI_ROPE = 4 };
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+
+struct GemmArgs {
+  const uint16_t* A = nullptr;  // [M, lda] bf16
+  const uint16_t* W = nullptr;  // [N, ldw] bf16 (row n = output column n)
+  void* C = nullptr;            // bf16 or f32 by epilogue
+  const float* bias = nullptr;  // [N] or null
+  int M = 0, N = 0, K = 0;
+  int lda = 0, ldw = 0, ldc = 0;
+  int epi = EPI_BF16;
+  int act = ACT_NONE;
+  // EPI_ROPE only
+  uint16_t* rope_q = nullptr;  // [H, rope_T, 64]
+  uint16_t* rope_k = nullptr;
+  uint16_t* rope_v = nullptr;
+  const int* rope_pos = nullptr;   // [M] position of each row in its sequence
+  const float* rope_cos = nullptr;  // [max_pos, 32]
+  const float* rope_sin = nullptr;
+  int rope_T = 0;
+  int rope_d = 0;
+};
+
+// Null when the shape is supported, else a message.
+const char* gemm_check(const GemmArgs& g);
+void gemm_launch(const GemmArgs& g, hipStream_t st);
+
+// Attention over packed variable-length rows. q, k, v are [H, Tq or Tk, 64] bf16 (head-major).
+// Queries are numbered by output slot; each work tile is up to 128 consecutive slots of one
+// sequence: {q0, q1, k0, k1} = slots [q0, q1) and the sequence's key range [k0, k1). Slot s reads
+// q row qkey[s] (or s when qkey is null), writes out row s, and sits at key index qkey[s] for
+// the window test. The decision head's pruned last layer uses qkey to attend from a few picked
+// tokens only; the encoder passes null.
+struct AttnTile {
+  int q0, q1, k0, k1;
+};
+struct AttnArgs {
+  const uint16_t* q = nullptr;
+  const uint16_t* k = nullptr;
+  const uint16_t* v = nullptr;
+  uint16_t* out = nullptr;  // [slots, ldo] bf16, head h at columns h*64 .. h*64+63
+  const AttnTile* tiles = nullptr;
+  const int* qkey = nullptr;  // [slots] q row / key index of each slot, or null for identity
+  int ntiles = 0;
+  int heads = 0;
+  int Tq = 0, Tk = 0;  // rows of the q buffer and of the k/v buffers (head strides)
+  int ldo = 0;
+  float scale = 0.125f;
+  int window = -1;  // < 0: global attention; else keys with |i - j| <= window
+};
+void attn_launch(const AttnArgs& a, hipStream_t st);
+
+// h[t] = LN(tok_emb[ids[t]]) (no bias), written as f32 and as bf16.
+void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
+                     uint16_t* x_out, hipStream_t st);
+
+// y = LN(x) (optional bias) over rows of d, x f32; y bf16 and/or f32 (null to skip). With
+// `rows` the input row of output row t is rows[t]. With `add_rowvec`, the f32 output also gets
+// add_rowvec[seg[t]] (the type embedding of the row's question), used to start the head stream.
+void layernorm_launch(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
+                      uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
+                      hipStream_t st);
+
+// Plain split (+ RoPE when cos/sin are given): qkv [T, 3d] bf16 -> q, k, v [H, T, 64] bf16.
+void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
+                       uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t st);
+
+// act[t, i] = gelu(wi[t, i]) * wi[t, I + i] for the un-interleaved Wi product.
+void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st);
+
+// Gather rows: out[r] = x[rows[r]] for f32 rows of d.
+void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out, hipStream_t st);
+
+// logits[r] = dot(x[r], w) + b, x bf16 [R, d], w f32 [d].
+void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st);
+
+}  // namespace s1

@@ -1,0 +1,779 @@
+// Host runtime of libsys1hip: checkpoint load, request planning and the kernel sequence of one
+// forward. The sequence follows MlxBackend::encode / head_forward / score / forward
+// (runtime/crates/laya-mlx/src/lib.rs:1525-1863) op for op, in the packed token layout that the
+// reference's `unpad` setting uses (Packing, lib.rs:894-943): activations are [T, ·] over the real
+// tokens only, and attention reads each row's token range directly instead of expanding to
+// [n, len].
+#include "model.hpp"
+
+#include <chrono>
+#include <cstdio>
+
+namespace s1 {
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(kBackend, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+Settings Settings::parse(const std::string& spec) {
+  Settings s;
+  size_t i = 0;
+  while (i <= spec.size()) {
+    size_t j = spec.find(',', i);
+    if (j == std::string::npos) j = spec.size();
+    std::string kv = spec.substr(i, j - i);
+    i = j + 1;
+    if (kv.empty()) {
+      if (j == spec.size()) break;
+      continue;
+    }
+    std::string key = kv, val;
+    bool has_val = false;
+    size_t eq = kv.find('=');
+    if (eq != std::string::npos) {
+      key = kv.substr(0, eq);
+      val = kv.substr(eq + 1);
+      has_val = true;
+    }
+    auto bad = [&](const std::string& what) { fail(kConfig, "hip settings: `" + kv + "`: " + what); };
+    auto flag = [&]() -> bool {
+      if (!has_val || val == "1") return true;
+      if (val == "0") return false;
+      bad("`" + val + "` is not 0 or 1");
+      return false;
+    };
+    auto number = [&](const std::string& v) -> size_t {
+      if (v.empty() || v.find_first_not_of("0123456789") != std::string::npos) bad("`" + v + "` is not a whole number");
+      return size_t(std::stoull(v));
+    };
+    if (key == "trace") s.trace = flag();
+    else if (key == "ops") s.ops = flag();
+    else if (key == "headprune") s.headprune = flag();
+    else if (key == "unpad") s.unpad = flag();
+    else if (key == "fuserope") s.fuserope = flag();
+    else if (key == "fusegeglu") s.fusegeglu = flag();
+    else if (key == "parallel_load") flag();  // read by the runtime (backend.rs:44-69); checked here too
+    else if (key == "pad") {
+      if (!has_val) bad("needs a value (`key=value`)");
+      s.pad = number(val);
+      if (s.pad == 0) bad("pad must be at least 1");
+    } else if (key == "buckets") {
+      if (!has_val) bad("needs a value (`key=value`)");
+      s.buckets.clear();
+      size_t a = 0;
+      while (a <= val.size()) {
+        size_t b = val.find(':', a);
+        if (b == std::string::npos) b = val.size();
+        s.buckets.push_back(number(val.substr(a, b - a)));
+        a = b + 1;
+      }
+      std::sort(s.buckets.begin(), s.buckets.end());
+    } else {
+      fail(kConfig, "hip settings: unknown setting `" + key + "` in `" + spec + "`");
+    }
+    if (j == spec.size()) break;
+  }
+  return s;
+}
+
+struct Model::Acts {
+  float* h;           // [T, d] residual stream (f32)
+  uint16_t* x;        // [T, d] normalised GEMM input
+  uint16_t *q, *k, *v;  // [H, T, 64]
+  uint16_t* qkv;      // [T, 3d]
+  uint16_t* att;      // [T, d]
+  uint16_t* mid;      // [T, max(2I, 4d)]
+  uint16_t* act;      // [T, I]
+  float* enc;         // [T, d] encoder output (encoder_hidden)
+  float* hh;          // [T, d] head stream
+  float* hp;          // [P, d] picked rows
+  uint16_t* xp;       // [P, d]
+  uint16_t* attp;     // [P, d]
+  uint16_t* midp;     // [P, 4d]
+  uint16_t* sx;       // [R, d]
+  uint16_t* s1;       // [R, S]
+  float* logits;      // [R]
+  float* pooled;      // [n, d]
+};
+
+Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, const std::string& enc_json,
+             const std::string& agent_json, const std::string& settings, int dev)
+    : device(dev) {
+  cfg = parse_model_config(enc_json, agent_json);
+  set = Settings::parse(settings);
+  if (cfg.head_dim() != 64)
+    fail(kConfig, "the HIP kernels need a head dim of 64; this encoder has " + std::to_string(cfg.head_dim()));
+  if (cfg.d != 512 && cfg.d != 1024 && cfg.d != 2048)
+    fail(kConfig, "the HIP kernels need hidden_size 512, 1024 or 2048; got " + std::to_string(cfg.d));
+  if (cfg.inter % 64 != 0)
+    fail(kConfig, "the HIP kernels need intermediate_size to be a multiple of 64; got " + std::to_string(cfg.inter));
+  if ((2 * cfg.inter) % 128 != 0)
+    fail(kConfig, "the HIP kernels need 2 * intermediate_size to be a multiple of 128");
+
+  SafeTensors st(st_bytes, st_len, what);
+  // Weights::verify (weights.rs:68-78)
+  {
+    auto names = st.names();
+    for (const char* prefix : {"encoder.", "type_emb.", "scorer.", "act_head."}) {
+      bool any = false;
+      for (const auto& n : names) any = any || n.rfind(prefix, 0) == 0;
+      if (!any)
+        fail(kWeights, std::string("checkpoint is missing '") + prefix +
+                           "' parameters; expected an RL Agent decision model");
+    }
+  }
+  const int64_t d = cfg.d, I = cfg.inter;
+  const auto& sc1 = st.get("scorer.1.weight");
+  if (sc1.shape.size() != 2 || sc1.shape[1] != d) fail(kWeights, what + ": scorer.1.weight must be [S, " + std::to_string(d) + "]");
+  scorer_width = int(sc1.shape[0]);
+  if (scorer_width % 128 != 0) fail(kConfig, "the HIP kernels need the scorer width to be a multiple of 128");
+
+  // ---- plan the weight arena
+  struct Item {
+    std::string name;
+    std::vector<int64_t> shape;
+    bool bf16;
+    int perm;  // 0 none, 1 Wi interleave, 2 take rows [r0, r0 + rows)
+    void** dst;
+  };
+  std::vector<Item> items;
+  auto addw = [&](const std::string& n, std::vector<int64_t> s, uint16_t** dst, int perm = 0) {
+    items.push_back({n, s, true, perm, reinterpret_cast<void**>(dst)});
+  };
+  auto addf = [&](const std::string& n, std::vector<int64_t> s, float** dst) {
+    items.push_back({n, s, false, 0, reinterpret_cast<void**>(dst)});
+  };
+  layers.resize(cfg.layers);
+  head.resize(cfg.head_layers);
+  addw("encoder.embeddings.tok_embeddings.weight", {cfg.vocab, d}, &tok_emb);
+  addf("encoder.embeddings.norm.weight", {d}, &emb_norm);
+  for (int i = 0; i < cfg.layers; ++i) {
+    std::string p = "encoder.layers." + std::to_string(i);
+    LayerWeights& L = layers[i];
+    L.local = cfg.layer_local[i];
+    if (i != 0) addf(p + ".attn_norm.weight", {d}, &L.attn_norm);
+    addw(p + ".attn.Wqkv.weight", {3 * d, d}, &L.wqkv);
+    addw(p + ".attn.Wo.weight", {d, d}, &L.wo);
+    addf(p + ".mlp_norm.weight", {d}, &L.mlp_norm);
+    addw(p + ".mlp.Wi.weight", {2 * I, d}, &L.wi, set.fusegeglu ? 1 : 0);
+    addw(p + ".mlp.Wo.weight", {d, I}, &L.wo2);
+  }
+  addf("encoder.final_norm.weight", {d}, &final_norm);
+  addf("type_emb.weight", {3, d}, &type_emb);
+  for (int j = 0; j < cfg.head_layers; ++j) {
+    std::string p = "head.layers." + std::to_string(j);
+    HeadWeights& H = head[j];
+    addf(p + ".norm1.weight", {d}, &H.n1w);
+    addf(p + ".norm1.bias", {d}, &H.n1b);
+    addw(p + ".self_attn.in_proj_weight", {3 * d, d}, &H.in_w);
+    addf(p + ".self_attn.in_proj_bias", {3 * d}, &H.in_b);
+    addw(p + ".self_attn.out_proj.weight", {d, d}, &H.out_w);
+    addf(p + ".self_attn.out_proj.bias", {d}, &H.out_b);
+    addf(p + ".norm2.weight", {d}, &H.n2w);
+    addf(p + ".norm2.bias", {d}, &H.n2b);
+    addw(p + ".linear1.weight", {4 * d, d}, &H.l1_w);
+    addf(p + ".linear1.bias", {4 * d}, &H.l1_b);
+    addw(p + ".linear2.weight", {d, 4 * d}, &H.l2_w);
+    addf(p + ".linear2.bias", {d}, &H.l2_b);
+  }
+  const int64_t S = scorer_width;
+  addf("scorer.0.weight", {d}, &sc0_w);
+  addf("scorer.0.bias", {d}, &sc0_b);
+  addw("scorer.1.weight", {S, d}, &sc1_w);
+  addf("scorer.1.bias", {S}, &sc1_b);
+  addf("scorer.3.weight", {1, S}, &sc3_w);
+  addf("scorer.3.bias", {1}, &sc3_b);
+
+  // Every tensor present with its expected shape before any device work (errors name the tensor).
+  for (const auto& it : items) {
+    const TensorView& tv = st.get(it.name);
+    if (tv.shape != it.shape) (void)st.to_f32(it.name, it.shape);  // throws the shape message
+  }
+
+  int ndev = 0;
+  hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+  if (dev < 0 || dev >= ndev) fail(kBackend, "no GPU with ordinal " + std::to_string(dev) + " (" + std::to_string(ndev) + " visible)");
+  hip_check(hipSetDevice(dev), "hipSetDevice");
+  hipDeviceProp_t prop;
+  hip_check(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+  if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+    fail(kBackend, std::string("libsys1hip is built for gfx950 (MI355X); device ") + std::to_string(dev) + " is " + prop.gcnArchName);
+  hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+
+  const int half = cfg.head_dim() / 2;
+  const size_t rope_bytes = align256(size_t(cfg.max_pos) * half * 4);
+  size_t total = 4 * rope_bytes;
+  std::vector<size_t> offs;
+  for (const auto& it : items) {
+    int64_t n = 1;
+    for (auto s : it.shape) n *= s;
+    offs.push_back(total);
+    total += align256(size_t(n) * (it.bf16 ? 2 : 4));
+  }
+  hip_check(hipMalloc(&wmem, total), "hipMalloc(weights)");
+  char* base = static_cast<char*>(wmem);
+
+  // ---- RoPE tables, with the reference kernel's angle arithmetic (split_rope.metal:46-49):
+  // inv_freq_i = exp2(-(i / half) * log2(theta)) and angle = p * inv_freq_i, both in f32; the
+  // cosine and sine of that f32 angle are taken in double and rounded once.
+  for (int which = 0; which < 2; ++which) {
+    const float theta = float(which == 0 ? cfg.global_theta : cfg.local_theta);
+    const float lbase = float(std::log2(double(theta)));
+    std::vector<float> inv(half), c(size_t(cfg.max_pos) * half), s(size_t(cfg.max_pos) * half);
+    for (int i = 0; i < half; ++i) {
+      const float ex = -(float(i) / float(half)) * lbase;
+      inv[i] = float(std::exp2(double(ex)));
+    }
+    for (int p = 0; p < cfg.max_pos; ++p)
+      for (int i = 0; i < half; ++i) {
+        const float ang = float(p) * inv[i];
+        c[size_t(p) * half + i] = float(std::cos(double(ang)));
+        s[size_t(p) * half + i] = float(std::sin(double(ang)));
+      }
+    rope_cos[which] = reinterpret_cast<float*>(base + (2 * which) * rope_bytes);
+    rope_sin[which] = reinterpret_cast<float*>(base + (2 * which + 1) * rope_bytes);
+    hip_check(hipMemcpy(rope_cos[which], c.data(), c.size() * 4, hipMemcpyHostToDevice), "upload rope");
+    hip_check(hipMemcpy(rope_sin[which], s.data(), s.size() * 4, hipMemcpyHostToDevice), "upload rope");
+  }
+
+  // ---- weights
+  std::vector<uint16_t> hb;
+  for (size_t k = 0; k < items.size(); ++k) {
+    const Item& it = items[k];
+    void* dptr = base + offs[k];
+    *it.dst = dptr;
+    if (!it.bf16) {
+      std::vector<float> f = st.to_f32(it.name, it.shape);
+      hip_check(hipMemcpy(dptr, f.data(), f.size() * 4, hipMemcpyHostToDevice), "upload weight");
+      continue;
+    }
+    const TensorView& tv = st.get(it.name);
+    if (tv.shape != it.shape) {
+      (void)st.to_f32(it.name, it.shape);  // throws with the shape message
+    }
+    const size_t n = size_t(tv.numel());
+    hb.resize(n);
+    if (tv.dtype == DType::BF16) {
+      std::memcpy(hb.data(), tv.data, n * 2);
+    } else {
+      std::vector<float> f = st.to_f32(it.name, it.shape);
+      for (size_t e = 0; e < n; ++e) hb[e] = f32_to_bf16(f[e]);
+    }
+    if (it.perm == 1) {
+      // Wi [2I, d] -> rows interleaved in blocks of 32: (x rows 32j.., gate rows I + 32j..).
+      std::vector<uint16_t> o(n);
+      const size_t rowb = size_t(d);
+      for (int64_t j = 0; j < I / 32; ++j) {
+        std::memcpy(&o[size_t(64 * j) * rowb], &hb[size_t(32 * j) * rowb], 32 * rowb * 2);
+        std::memcpy(&o[size_t(64 * j + 32) * rowb], &hb[size_t(I + 32 * j) * rowb], 32 * rowb * 2);
+      }
+      hb.swap(o);
+    }
+    hip_check(hipMemcpy(dptr, hb.data(), n * 2, hipMemcpyHostToDevice), "upload weight");
+  }
+
+  char nb[64];
+  std::snprintf(nb, sizeof nb, "hip(gfx950,bf16)");
+  name = nb;
+  kernels = "mfma";
+  if (set.fuserope) kernels += ",fuserope";
+  kernels += ",band";
+  if (set.fusegeglu) kernels += ",fusegeglu";
+  if (set.headprune) kernels += ",headprune";
+}
+
+Model::~Model() {
+  // Teardown: errors here have nowhere to go, the process keeps running.
+  if (stream) (void)hipStreamSynchronize(stream);
+  for (auto& r : pending) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (auto e : event_pool) (void)hipEventDestroy(e);
+  if (wmem) (void)hipFree(wmem);
+  if (amem) (void)hipFree(amem);
+  if (dmeta) (void)hipFree(dmeta);
+  if (hmeta) (void)hipHostFree(hmeta);
+  if (hout) (void)hipHostFree(hout);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+size_t Model::padded_len(size_t len) const {
+  for (size_t b : set.buckets)
+    if (b >= len) return b;
+  return (len + set.pad - 1) / set.pad * set.pad;
+}
+
+Packed pack_batch(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* mask, const uint64_t* seq_lens,
+                  const uint32_t* marker_pos, const uint64_t* marker_count, int max_pos) {
+  Packed k;
+  k.row_start.resize(n + 1);
+  if (n == 0) return k;
+  if (len == 0) fail(kBatch, "batch: len is 0 with n > 0");
+  if (!mask || !seq_lens || !marker_count || (kmax && !marker_pos)) fail(kBatch, "batch: a required array is NULL");
+  int64_t T = 0;
+  for (uint32_t r = 0; r < n; ++r) {
+    const uint64_t sl = seq_lens[r];
+    if (sl == 0 || sl > len)
+      fail(kBatch, "batch: seq_lens[" + std::to_string(r) + "] = " + std::to_string(sl) + " is not in 1..len");
+    if (sl > uint64_t(max_pos))
+      fail(kBatch, "batch: row " + std::to_string(r) + " has " + std::to_string(sl) +
+                       " tokens, past max_position_embeddings " + std::to_string(max_pos));
+    for (uint32_t q = 0; q < len; ++q) {
+      const uint32_t want = q < sl ? 1u : 0u;
+      if (mask[size_t(r) * len + q] != want)
+        fail(kBatch, "batch: attention_mask of row " + std::to_string(r) +
+                         " is not seq_lens ones followed by zeros (right-padded rows only)");
+    }
+    if (marker_count[r] > kmax) fail(kBatch, "batch: marker_count[" + std::to_string(r) + "] exceeds kmax");
+    for (uint64_t j = 0; j < marker_count[r]; ++j)
+      if (marker_pos[size_t(r) * kmax + j] >= sl)
+        fail(kBatch, "batch: marker_pos of row " + std::to_string(r) + " points past the row");
+    k.row_start[r] = int(T);
+    T += int64_t(sl);
+    if (T > (int64_t(1) << 30)) fail(kBatch, "batch: too many tokens");
+  }
+  k.row_start[n] = int(T);
+  k.T = int(T);
+  k.pack.reserve(size_t(T));
+  k.row.reserve(size_t(T));
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint64_t q = 0; q < seq_lens[r]; ++q) {
+      k.pack.push_back(int(size_t(r) * len + q));
+      k.row.push_back(int(r));
+    }
+  k.scorer_rows.reserve(size_t(n) * (1 + kmax));
+  for (uint32_t r = 0; r < n; ++r) {
+    k.scorer_rows.push_back(k.row_start[r]);
+    for (uint32_t j = 0; j < kmax; ++j)
+      k.scorer_rows.push_back(k.row_start[r] + (j < marker_count[r] ? int(marker_pos[size_t(r) * kmax + j]) : 0));
+  }
+  return k;
+}
+
+Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, const uint32_t* mask,
+                 const uint64_t* seq_lens, const uint32_t* marker_pos, const uint64_t* marker_count,
+                 const uint32_t* qtype) const {
+  Plan p;
+  p.n = int(n);
+  p.len = int(len);
+  p.kmax = int(kmax);
+  if (n == 0) return p;
+  if (!ids || !qtype) fail(kBatch, "batch: a required array is NULL");
+  Packed pk = pack_batch(n, len, kmax, mask, seq_lens, marker_pos, marker_count, cfg.max_pos);
+  for (uint32_t r = 0; r < n; ++r)
+    if (qtype[r] > 2) fail(kBatch, "batch: qtype[" + std::to_string(r) + "] is not 0, 1 or 2");
+  p.row_start = pk.row_start;
+  const int64_t T = pk.T;
+  p.T = int(T);
+  p.P = set.headprune ? int(n * (1 + kmax)) : 0;
+  p.R = int(n * kmax);
+
+  std::vector<int>& m = p.meta;
+  m.reserve(size_t(3 * T) + 64);
+  p.off_ids = m.size();
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint64_t q = 0; q < seq_lens[r]; ++q) {
+      const uint32_t id = ids[size_t(r) * len + q];
+      if (id >= uint32_t(cfg.vocab))
+        fail(kBatch, "batch: token id " + std::to_string(id) + " in row " + std::to_string(r) + " is past the vocabulary");
+      m.push_back(int(id));
+    }
+  p.off_pos = m.size();
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint64_t q = 0; q < seq_lens[r]; ++q) m.push_back(int(q));
+  p.off_seg = m.size();
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint64_t q = 0; q < seq_lens[r]; ++q) m.push_back(int(qtype[r]));
+  auto pad4 = [&]() {
+    while (m.size() % 4) m.push_back(0);
+  };
+  pad4();
+  p.off_tiles = m.size();
+  for (uint32_t r = 0; r < n; ++r) {
+    const int rs = p.row_start[r], re = p.row_start[r + 1];
+    for (int q0 = rs; q0 < re; q0 += 128) {
+      m.push_back(q0);
+      m.push_back(std::min(q0 + 128, re));
+      m.push_back(rs);
+      m.push_back(re);
+      ++p.ntiles;
+    }
+  }
+  const int per = 1 + int(kmax);
+  if (set.headprune) {
+    p.off_ptiles = m.size();
+    for (uint32_t r = 0; r < n; ++r) {
+      const int s0 = int(r) * per, s1 = s0 + per;
+      for (int q0 = s0; q0 < s1; q0 += 128) {
+        m.push_back(q0);
+        m.push_back(std::min(q0 + 128, s1));
+        m.push_back(p.row_start[r]);
+        m.push_back(p.row_start[r + 1]);
+        ++p.nptiles;
+      }
+    }
+    p.off_picked = m.size();
+    m.insert(m.end(), pk.scorer_rows.begin(), pk.scorer_rows.end());
+  }
+  p.off_scorer = m.size();
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t k = 0; k < kmax; ++k) {
+      if (set.headprune)
+        m.push_back(int(r) * per + 1 + int(k));
+      else
+        m.push_back(pk.scorer_rows[size_t(r) * per + 1 + k]);
+    }
+  p.off_pooled = m.size();
+  for (uint32_t r = 0; r < n; ++r) m.push_back(set.headprune ? int(r) * per : p.row_start[r]);
+  pad4();
+  return p;
+}
+
+void Model::upload(const Plan& p) {
+  const size_t bytes = p.meta.size() * 4;
+  if (bytes > hmeta_cap) {
+    if (hmeta) hip_check(hipHostFree(hmeta), "hipHostFree");
+    hmeta_cap = std::max(bytes, hmeta_cap * 3 / 2);
+    hip_check(hipHostMalloc(&hmeta, hmeta_cap, hipHostMallocDefault), "hipHostMalloc(meta)");
+  }
+  if (bytes > dmeta_cap) {
+    if (dmeta) hip_check(hipFree(dmeta), "hipFree");
+    dmeta_cap = std::max(bytes, dmeta_cap * 3 / 2);
+    hip_check(hipMalloc(&dmeta, dmeta_cap), "hipMalloc(meta)");
+  }
+  // The previous request's copy out of the staging buffer has finished: every call ends with a
+  // stream synchronisation.
+  std::memcpy(hmeta, p.meta.data(), bytes);
+  hip_check(hipMemcpyAsync(dmeta, hmeta, bytes, hipMemcpyHostToDevice, stream), "upload batch");
+}
+
+Model::Acts Model::arena(const Plan& p) {
+  const size_t T = size_t(p.T), P = size_t(p.P), R = size_t(p.R), n = size_t(p.n);
+  const size_t d = size_t(cfg.d), I = size_t(cfg.inter), S = size_t(scorer_width);
+  const size_t midw = std::max(2 * I, 4 * d);
+  size_t sizes[] = {T * d * 4, T * d * 2, T * d * 2, T * d * 2, T * d * 2, T * 3 * d * 2, T * d * 2,
+                    T * midw * 2, T * I * 2, T * d * 4, T * d * 4, P * d * 4, P * d * 2, P * d * 2,
+                    P * 4 * d * 2, R * d * 2, R * S * 2, R * 4, n * d * 4};
+  constexpr int NS = sizeof(sizes) / sizeof(sizes[0]);
+  size_t off[NS], total = 0;
+  for (int i = 0; i < NS; ++i) {
+    off[i] = total;
+    total += align256(std::max<size_t>(sizes[i], 16));
+  }
+  if (total > acap) {
+    if (amem) {
+      hip_check(hipStreamSynchronize(stream), "sync");
+      hip_check(hipFree(amem), "hipFree(arena)");
+      amem = nullptr;
+    }
+    const size_t cap = std::max(total, acap * 3 / 2);
+    hip_check(hipMalloc(&amem, cap), "hipMalloc(activations)");
+    acap = cap;
+  }
+  char* b = static_cast<char*>(amem);
+  Acts a;
+  a.h = reinterpret_cast<float*>(b + off[0]);
+  a.x = reinterpret_cast<uint16_t*>(b + off[1]);
+  a.q = reinterpret_cast<uint16_t*>(b + off[2]);
+  a.k = reinterpret_cast<uint16_t*>(b + off[3]);
+  a.v = reinterpret_cast<uint16_t*>(b + off[4]);
+  a.qkv = reinterpret_cast<uint16_t*>(b + off[5]);
+  a.att = reinterpret_cast<uint16_t*>(b + off[6]);
+  a.mid = reinterpret_cast<uint16_t*>(b + off[7]);
+  a.act = reinterpret_cast<uint16_t*>(b + off[8]);
+  a.enc = reinterpret_cast<float*>(b + off[9]);
+  a.hh = reinterpret_cast<float*>(b + off[10]);
+  a.hp = reinterpret_cast<float*>(b + off[11]);
+  a.xp = reinterpret_cast<uint16_t*>(b + off[12]);
+  a.attp = reinterpret_cast<uint16_t*>(b + off[13]);
+  a.midp = reinterpret_cast<uint16_t*>(b + off[14]);
+  a.sx = reinterpret_cast<uint16_t*>(b + off[15]);
+  a.s1 = reinterpret_cast<uint16_t*>(b + off[16]);
+  a.logits = reinterpret_cast<float*>(b + off[17]);
+  a.pooled = reinterpret_cast<float*>(b + off[18]);
+  return a;
+}
+
+template <class F>
+void Model::op(const char* nm, F&& f) {
+  if (!set.ops) {
+    f();
+    return;
+  }
+  auto ev = [&]() {
+    hipEvent_t e;
+    if (!event_pool.empty()) {
+      e = event_pool.back();
+      event_pool.pop_back();
+    } else {
+      hip_check(hipEventCreate(&e), "hipEventCreate");
+    }
+    return e;
+  };
+  OpRec r{nm, ev(), ev()};
+  hip_check(hipEventRecord(r.a, stream), "hipEventRecord");
+  f();
+  hip_check(hipEventRecord(r.b, stream), "hipEventRecord");
+  pending.push_back(r);
+}
+
+void Model::collect_stats() {
+  for (auto& r : pending) {
+    float ms = 0.0f;
+    hip_check(hipEventElapsedTime(&ms, r.a, r.b), "hipEventElapsedTime");
+    bool found = false;
+    for (auto& s : stats)
+      if (s.first == r.name) {
+        s.second.first += 1;
+        s.second.second += ms;
+        found = true;
+        break;
+      }
+    if (!found) stats.push_back({r.name, {1, double(ms)}});
+    event_pool.push_back(r.a);
+    event_pool.push_back(r.b);
+  }
+  pending.clear();
+}
+
+namespace {
+
+void gemm(hipStream_t st, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc, const float* bias,
+          int M, int N, int epi, int act = ACT_NONE) {
+  GemmArgs g;
+  g.A = A;
+  g.W = W;
+  g.C = C;
+  g.bias = bias;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = lda;
+  g.ldw = K;
+  g.ldc = ldc;
+  g.epi = epi;
+  g.act = act;
+  if (const char* e = gemm_check(g)) fail(kBackend, e);
+  gemm_launch(g, st);
+}
+
+}  // namespace
+
+void Model::run_encoder(const Plan& p, const Acts& a) {
+  const int T = p.T, d = cfg.d, I = cfg.inter, H = cfg.heads;
+  const float eps = float(cfg.eps);
+  const int* ids = dmeta + p.off_ids;
+  const int* pos = dmeta + p.off_pos;
+  const AttnTile* tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_tiles);
+
+  // h = LN(tok_emb[ids]) (lib.rs:1534-1551); x = h for layer 0, which has no attn_norm.
+  op("embed_ln", [&] { embed_ln_launch(tok_emb, ids, emb_norm, eps, T, d, a.h, a.x, stream); });
+  for (int l = 0; l < cfg.layers; ++l) {
+    const LayerWeights& L = layers[l];
+    const int tw = L.local ? 1 : 0;
+    if (L.attn_norm)
+      op("attn_norm", [&] {
+        layernorm_launch(a.h, nullptr, L.attn_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+      });
+    if (set.fuserope) {
+      op("wqkv_rope", [&] {
+        GemmArgs g;
+        g.A = a.x;
+        g.W = L.wqkv;
+        g.M = T;
+        g.N = 3 * d;
+        g.K = d;
+        g.lda = d;
+        g.ldw = d;
+        g.epi = EPI_ROPE;
+        g.rope_q = a.q;
+        g.rope_k = a.k;
+        g.rope_v = a.v;
+        g.rope_pos = pos;
+        g.rope_cos = rope_cos[tw];
+        g.rope_sin = rope_sin[tw];
+        g.rope_T = T;
+        g.rope_d = d;
+        if (const char* e = gemm_check(g)) fail(kBackend, e);
+        gemm_launch(g, stream);
+      });
+    } else {
+      op("wqkv", [&] { gemm(stream, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
+      op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, stream); });
+    }
+    op(L.local ? "attn_local" : "attn_global", [&] {
+      AttnArgs at;
+      at.q = a.q;
+      at.k = a.k;
+      at.v = a.v;
+      at.out = a.att;
+      at.tiles = tiles;
+      at.ntiles = p.ntiles;
+      at.heads = H;
+      at.Tq = T;
+      at.Tk = T;
+      at.ldo = d;
+      at.scale = 1.0f / std::sqrt(float(cfg.head_dim()));
+      at.window = L.local ? cfg.window() : -1;
+      attn_launch(at, stream);
+    });
+    // h = h + att . Wo^T (lib.rs:1666)
+    op("wo", [&] { gemm(stream, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID); });
+    op("mlp_norm", [&] {
+      layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+    });
+    if (set.fusegeglu) {
+      op("wi_geglu", [&] { gemm(stream, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
+    } else {
+      op("wi", [&] { gemm(stream, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
+      op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream); });
+    }
+    // h = h + act . Wo2^T (lib.rs:1675)
+    op("wo2", [&] { gemm(stream, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID); });
+  }
+}
+
+void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
+  if (p.n == 0) return;
+  const auto t0 = std::chrono::steady_clock::now();
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  upload(p);
+  Acts a = arena(p);
+  const int T = p.T, d = cfg.d, P = p.P, R = p.R, n = p.n, S = scorer_width;
+  const float eps = float(cfg.eps);
+  const int* seg = dmeta + p.off_seg;
+  run_encoder(p, a);
+  // final_norm (lib.rs:1689), then h + type_emb[qtype] per row (lib.rs:1702-1709) in one pass.
+  op("final_norm", [&] {
+    layernorm_launch(a.h, nullptr, final_norm, nullptr, eps, T, d, nullptr, nullptr, type_emb, seg, a.hh, stream);
+  });
+  const AttnTile* tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_tiles);
+  const float hscale = 1.0f / std::sqrt(float(d / cfg.head_nheads()));  // head_scale (lib.rs:576-578)
+  const int nh = cfg.head_layers;
+  for (int j = 0; j < nh; ++j) {
+    const HeadWeights& Hw = head[j];
+    const bool pruned = set.headprune && j + 1 == nh;
+    // x = norm1(h); qkv = x . in_proj^T + b; split heads (lib.rs:1726-1741)
+    op("head_norm1", [&] {
+      layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+    });
+    op("head_in_proj", [&] { gemm(stream, a.x, d, Hw.in_w, d, a.qkv, 3 * d, Hw.in_b, T, 3 * d, EPI_BF16); });
+    op("head_split", [&] { split_rope_launch(a.qkv, T, d, nullptr, nullptr, nullptr, a.q, a.k, a.v, stream); });
+    if (!pruned) {
+      op("head_attn", [&] {
+        AttnArgs at;
+        at.q = a.q;
+        at.k = a.k;
+        at.v = a.v;
+        at.out = a.att;
+        at.tiles = tiles;
+        at.ntiles = p.ntiles;
+        at.heads = cfg.head_nheads();
+        at.Tq = T;
+        at.Tk = T;
+        at.ldo = d;
+        at.scale = hscale;
+        attn_launch(at, stream);
+      });
+      op("head_out_proj", [&] { gemm(stream, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
+      op("head_norm2", [&] {
+        layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+      });
+      op("head_linear1", [&] { gemm(stream, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(stream, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
+    } else {
+      // headprune (lib.rs:1728-1748): every token supplies k and v; queries, out_proj, norm2 and
+      // the FFN run at rows {0, markers} only.
+      const int* picked = dmeta + p.off_picked;
+      op("head_attn", [&] {
+        AttnArgs at;
+        at.q = a.q;
+        at.k = a.k;
+        at.v = a.v;
+        at.out = a.attp;
+        at.tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_ptiles);
+        at.ntiles = p.nptiles;
+        at.qkey = picked;
+        at.heads = cfg.head_nheads();
+        at.Tq = T;
+        at.Tk = T;
+        at.ldo = d;
+        at.scale = hscale;
+        attn_launch(at, stream);
+      });
+      op("head_pick", [&] { gather_f32_launch(a.hh, picked, P, d, a.hp, stream); });
+      op("head_out_proj", [&] { gemm(stream, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
+      op("head_norm2", [&] {
+        layernorm_launch(a.hp, nullptr, Hw.n2w, Hw.n2b, 1e-5f, P, d, a.xp, nullptr, nullptr, nullptr, nullptr, stream);
+      });
+      op("head_linear1", [&] { gemm(stream, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(stream, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
+    }
+  }
+  // score (lib.rs:1768-1800): LN_b at the marker rows, scorer1 + GELU, scorer3; pooled row 0.
+  const float* src = set.headprune ? a.hp : a.hh;
+  const int* srows = dmeta + p.off_scorer;
+  const int* prows = dmeta + p.off_pooled;
+  if (R > 0) {
+    op("scorer_norm", [&] {
+      layernorm_launch(src, srows, sc0_w, sc0_b, 1e-5f, R, d, a.sx, nullptr, nullptr, nullptr, nullptr, stream);
+    });
+    op("scorer1", [&] { gemm(stream, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
+    op("scorer3", [&] { rowdot_launch(a.s1, sc3_w, sc3_b, R, S, a.logits, stream); });
+  }
+  op("pooled", [&] { gather_f32_launch(src, prows, n, d, a.pooled, stream); });
+  hip_check(hipGetLastError(), "kernel launch");
+
+  const size_t out_bytes = size_t(R) * 4 + size_t(n) * d * 4;
+  if (out_bytes > hout_cap) {
+    if (hout) hip_check(hipHostFree(hout), "hipHostFree");
+    hout_cap = std::max(out_bytes, hout_cap * 3 / 2);
+    hip_check(hipHostMalloc(&hout, hout_cap, hipHostMallocDefault), "hipHostMalloc(out)");
+  }
+  float* hl = static_cast<float*>(hout);
+  float* hpool = hl + R;
+  if (R > 0) hip_check(hipMemcpyAsync(hl, a.logits, size_t(R) * 4, hipMemcpyDeviceToHost, stream), "download logits");
+  hip_check(hipMemcpyAsync(hpool, a.pooled, size_t(n) * d * 4, hipMemcpyDeviceToHost, stream), "download pooled");
+  hip_check(hipStreamSynchronize(stream), "forward");
+  if (set.ops) collect_stats();
+  std::memcpy(logits_out, hl, size_t(R) * 4);
+  std::memcpy(pooled_out, hpool, size_t(n) * d * 4);
+  if (set.trace) {
+    const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    std::fprintf(stderr, "forward n=%d len=%d T=%d us=%.1f\n", p.n, p.len, p.T, us);
+  }
+}
+
+void Model::encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden) {
+  if (p.n == 0) return;
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  upload(p);
+  Acts a = arena(p);
+  const int T = p.T, d = cfg.d;
+  run_encoder(p, a);
+  op("final_norm", [&] {
+    layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, nullptr, nullptr,
+                     nullptr, stream);
+  });
+  hip_check(hipGetLastError(), "kernel launch");
+  std::vector<float> packed(size_t(T) * d);
+  hip_check(hipMemcpyAsync(packed.data(), a.enc, packed.size() * 4, hipMemcpyDeviceToHost, stream), "download hidden");
+  hip_check(hipStreamSynchronize(stream), "encoder_hidden");
+  if (set.ops) collect_stats();
+  // Expand [T, d] -> [n, len, d]; padding positions are not computed and read 0.
+  std::memset(hidden, 0, size_t(p.n) * p.len * d * 4);
+  for (int r = 0; r < p.n; ++r) {
+    const int rs = p.row_start[r], sl = p.row_start[r + 1] - rs;
+    std::memcpy(hidden + size_t(r) * p.len * d, packed.data() + size_t(rs) * d, size_t(sl) * d * 4);
+  }
+  (void)mask;
+}
+
+}  // namespace s1

@@ -1,0 +1,144 @@
+// The loaded decision model on one GPU: device weights, activation arena, stream and the
+// per-request plan. Mirrors MlxBackend (runtime/crates/laya-mlx/src/lib.rs:960-1879).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "safetensors.hpp"
+
+namespace s1 {
+
+// Strict settings, parsed like the reference's Knobs (lib.rs:155-259): a comma list of `key` or
+// `key=value`, the last mention wins, an unknown key is a config error.
+struct Settings {
+  bool trace = false;      // print per-forward timings to stderr
+  bool ops = false;        // per-kernel HIP-event timing (s1_op_stats)
+  bool headprune = true;   // last head layer only at the scorer's rows (lib.rs:1728-1748)
+  bool unpad = true;       // accepted; the HIP path always runs the packed token layout
+  bool fuserope = true;    // RoPE + split fused into the Wqkv GEMM epilogue
+  bool fusegeglu = true;   // GeGLU fused into the Wi GEMM epilogue (Wi rows interleaved at load)
+  size_t pad = 1;          // padded_len multiple
+  std::vector<size_t> buckets;
+  static Settings parse(const std::string& spec);
+};
+
+struct LayerWeights {
+  uint16_t* wqkv = nullptr;  // [3d, d]
+  uint16_t* wo = nullptr;    // [d, d]
+  uint16_t* wi = nullptr;    // [2I, d], rows interleaved by 32 when fusegeglu
+  uint16_t* wo2 = nullptr;   // [d, I]
+  float* attn_norm = nullptr;  // null for layer 0
+  float* mlp_norm = nullptr;
+  bool local = false;
+};
+
+struct HeadWeights {
+  float *n1w, *n1b, *n2w, *n2b;
+  uint16_t* in_w;
+  float* in_b;
+  uint16_t* out_w;
+  float* out_b;
+  uint16_t* l1_w;
+  float* l1_b;
+  uint16_t* l2_w;
+  float* l2_b;
+};
+
+// The packed token layout of a right-padded batch (Packing::new and MlxBackend::scorer_rows,
+// runtime/crates/laya-mlx/src/lib.rs:894-943, 1502-1521). Validates the batch on the way.
+struct Packed {
+  int T = 0;
+  std::vector<int> row_start;    // [n + 1] packed index of position 0 of each row, then T
+  std::vector<int> pack;         // [T] padded flat index r * len + pos of each packed token
+  std::vector<int> row;          // [T] row of each packed token
+  std::vector<int> scorer_rows;  // [n * (1 + kmax)] packed index of position 0, then the kmax
+                                 // marker slots (slots past marker_count point at position 0)
+};
+Packed pack_batch(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* mask, const uint64_t* seq_lens,
+                  const uint32_t* marker_pos, const uint64_t* marker_count, int max_pos);
+
+// A validated batch in packed form, plus every index table the kernels read.
+struct Plan {
+  int n = 0, len = 0, kmax = 0;
+  int T = 0;  // real tokens
+  int P = 0;  // picked rows of the pruned head layer (n * (1 + kmax))
+  int R = 0;  // scorer rows (n * kmax)
+  std::vector<int> row_start;  // [n + 1]
+  // device-bound tables (int32), concatenated in `meta`
+  std::vector<int> meta;
+  size_t off_ids = 0, off_pos = 0, off_seg = 0, off_tiles = 0, off_ptiles = 0, off_picked = 0, off_scorer = 0,
+         off_pooled = 0, off_pseg = 0;
+  int ntiles = 0, nptiles = 0;
+};
+
+struct Model {
+  ModelConfig cfg;
+  Settings set;
+  int device = 0;
+  int scorer_width = 0;
+  hipStream_t stream = nullptr;
+  std::string name, kernels;
+
+  // weights (one device allocation)
+  void* wmem = nullptr;
+  uint16_t* tok_emb = nullptr;
+  float* emb_norm = nullptr;
+  std::vector<LayerWeights> layers;
+  float* final_norm = nullptr;
+  float* type_emb = nullptr;  // [3, d] f32
+  std::vector<HeadWeights> head;
+  float *sc0_w = nullptr, *sc0_b = nullptr;
+  uint16_t* sc1_w = nullptr;
+  float* sc1_b = nullptr;
+  float* sc3_w = nullptr;
+  float* sc3_b = nullptr;
+  float* rope_cos[2] = {nullptr, nullptr};  // [max_pos, hd/2] for global (0) and local (1)
+  float* rope_sin[2] = {nullptr, nullptr};
+
+  // activation arena, grown on demand
+  void* amem = nullptr;
+  size_t acap = 0;
+  // pinned host staging
+  void* hmeta = nullptr;
+  size_t hmeta_cap = 0;
+  void* hout = nullptr;
+  size_t hout_cap = 0;
+  int* dmeta = nullptr;
+  size_t dmeta_cap = 0;
+
+  // per-kernel timing (Settings::ops)
+  struct OpRec {
+    const char* name;
+    hipEvent_t a, b;
+  };
+  std::vector<OpRec> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::vector<std::pair<std::string, std::pair<uint64_t, double>>> stats;
+
+  Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, const std::string& enc_json,
+        const std::string& agent_json, const std::string& settings, int device);
+  ~Model();
+
+  Plan plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, const uint32_t* mask,
+            const uint64_t* seq_lens, const uint32_t* marker_pos, const uint64_t* marker_count,
+            const uint32_t* qtype) const;
+  void forward(const Plan& p, float* logits, float* pooled);
+  void encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden);
+  size_t padded_len(size_t len) const;
+
+ private:
+  struct Acts;
+  Acts arena(const Plan& p);
+  void upload(const Plan& p);
+  void run_encoder(const Plan& p, const Acts& a);
+  template <class F>
+  void op(const char* name, F&& f);
+  void collect_stats();
+};
+
+}  // namespace s1

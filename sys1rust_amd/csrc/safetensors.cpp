@@ -1,0 +1,132 @@
+#include "safetensors.hpp"
+
+#include <algorithm>
+
+namespace s1 {
+
+SafeTensors::SafeTensors(const uint8_t* bytes, size_t len, const std::string& what) : what_(what) {
+  if (len < 8) fail(kWeights, what + ": file is too short for a safetensors header (" + std::to_string(len) + " bytes)");
+  uint64_t hlen = 0;
+  for (int i = 0; i < 8; ++i) hlen |= uint64_t(bytes[i]) << (8 * i);
+  if (hlen > len - 8) fail(kWeights, what + ": header length " + std::to_string(hlen) + " runs past the end of the file");
+  JsonValue h;
+  try {
+    JsonParser p(reinterpret_cast<const char*>(bytes + 8), size_t(hlen));
+    h = p.parse();
+  } catch (const std::exception& e) {
+    fail(kWeights, what + ": bad safetensors header: " + e.what());
+  }
+  if (h.kind != JsonValue::Object) fail(kWeights, what + ": safetensors header is not an object");
+  const uint8_t* base = bytes + 8 + hlen;
+  size_t avail = len - 8 - size_t(hlen);
+  for (const auto& kv : h.obj) {
+    if (kv.first == "__metadata__") continue;
+    const JsonValue& t = kv.second;
+    const JsonValue* dt = t.get("dtype");
+    const JsonValue* sh = t.get("shape");
+    const JsonValue* of = t.get("data_offsets");
+    if (!dt || dt->kind != JsonValue::String || !sh || sh->kind != JsonValue::Array || !of ||
+        of->kind != JsonValue::Array || of->arr.size() != 2)
+      fail(kWeights, what + ": tensor '" + kv.first + "' has a malformed header entry");
+    TensorView tv;
+    size_t esize;
+    if (dt->str == "F32") { tv.dtype = DType::F32; esize = 4; }
+    else if (dt->str == "F16") { tv.dtype = DType::F16; esize = 2; }
+    else if (dt->str == "BF16") { tv.dtype = DType::BF16; esize = 2; }
+    else if (dt->str == "F64") { tv.dtype = DType::F64; esize = 8; }
+    else fail(kWeights, what + ": tensor '" + kv.first + "': unsupported dtype " + dt->str);
+    for (const auto& s : sh->arr) {
+      if (s.kind != JsonValue::Number || !s.is_int || s.i < 0)
+        fail(kWeights, what + ": tensor '" + kv.first + "' has a bad shape");
+      tv.shape.push_back(s.i);
+    }
+    const JsonValue& b = of->arr[0];
+    const JsonValue& e = of->arr[1];
+    if (b.kind != JsonValue::Number || e.kind != JsonValue::Number || !b.is_int || !e.is_int || b.i < 0 || e.i < b.i)
+      fail(kWeights, what + ": tensor '" + kv.first + "' has bad data offsets");
+    if (size_t(e.i) > avail)
+      fail(kWeights, what + ": tensor '" + kv.first + "' runs past the end of the file (truncated?)");
+    tv.nbytes = size_t(e.i - b.i);
+    if (tv.nbytes != size_t(tv.numel()) * esize)
+      fail(kWeights, what + ": tensor '" + kv.first + "' byte length does not match its shape");
+    tv.data = base + b.i;
+    map_[kv.first] = tv;
+  }
+}
+
+const TensorView& SafeTensors::get(const std::string& name) const {
+  auto it = map_.find(name);
+  if (it == map_.end()) fail(kWeights, what_ + ": missing tensor '" + name + "'");
+  return it->second;
+}
+
+std::vector<std::string> SafeTensors::names() const {
+  std::vector<std::string> n;
+  for (const auto& kv : map_) n.push_back(kv.first);
+  std::sort(n.begin(), n.end());
+  return n;
+}
+
+std::vector<float> SafeTensors::to_f32(const std::string& name, const std::vector<int64_t>& want) const {
+  const TensorView& t = get(name);
+  if (t.shape != want) {
+    std::string got, exp;
+    for (auto s : t.shape) got += std::to_string(s) + ",";
+    for (auto s : want) exp += std::to_string(s) + ",";
+    fail(kWeights, what_ + ": tensor '" + name + "' has shape [" + got + "], expected [" + exp + "]");
+  }
+  std::vector<float> out(size_t(t.numel()));
+  const uint8_t* p = t.data;
+  switch (t.dtype) {
+    case DType::F32:
+      std::memcpy(out.data(), p, out.size() * 4);
+      break;
+    case DType::F16:
+      for (size_t i = 0; i < out.size(); ++i) out[i] = f16_to_f32(uint16_t(p[2 * i] | (p[2 * i + 1] << 8)));
+      break;
+    case DType::BF16:
+      for (size_t i = 0; i < out.size(); ++i) out[i] = bf16_to_f32(uint16_t(p[2 * i] | (p[2 * i + 1] << 8)));
+      break;
+    case DType::F64:
+      for (size_t i = 0; i < out.size(); ++i) {
+        double d;
+        std::memcpy(&d, p + 8 * i, 8);
+        out[i] = float(d);
+      }
+      break;
+  }
+  return out;
+}
+
+std::vector<uint8_t> write_safetensors_bf16(const std::vector<OutTensor>& ts) {
+  std::string h = "{\"__metadata__\":{\"format\":\"pt\"}";
+  size_t off = 0;
+  for (const auto& t : ts) {
+    h += ",\"" + t.name + "\":{\"dtype\":\"BF16\",\"shape\":[";
+    int64_t numel = 1;
+    for (size_t i = 0; i < t.shape.size(); ++i) {
+      h += (i ? "," : "") + std::to_string(t.shape[i]);
+      numel *= t.shape[i];
+    }
+    size_t nb = size_t(numel) * 2;
+    h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + nb) + "]}";
+    off += nb;
+  }
+  h += "}";
+  while ((h.size() + 8) % 8) h.push_back(' ');
+  std::vector<uint8_t> out(8 + h.size() + off);
+  uint64_t hl = h.size();
+  for (int i = 0; i < 8; ++i) out[i] = uint8_t(hl >> (8 * i));
+  std::memcpy(out.data() + 8, h.data(), h.size());
+  uint8_t* p = out.data() + 8 + h.size();
+  for (const auto& t : ts) {
+    int64_t numel = 1;
+    for (auto s : t.shape) numel *= s;
+    // A tensor without a payload (size queries) leaves zeros.
+    if (!t.bf16.empty()) std::memcpy(p, t.bf16.data(), t.bf16.size() * 2);  // little-endian host
+    p += size_t(numel) * 2;
+  }
+  return out;
+}
+
+}  // namespace s1

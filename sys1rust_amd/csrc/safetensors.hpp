@@ -1,0 +1,60 @@
+// safetensors reading (checkpoint load) and writing (the synthetic checkpoint generator).
+//
+// Format: an 8-byte little-endian header length, a JSON header mapping each tensor name to
+// {dtype, shape, data_offsets:[begin,end]} (offsets relative to the byte after the header), and
+// the tensor bytes. The reader mirrors laya_core::Weights::open / verify / to_f32
+// (runtime/crates/laya-core/src/weights.rs:22-103): a truncated file or a header that does not
+// fit its data is an error naming the problem, never a crash.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+
+namespace s1 {
+
+enum class DType { F32, F16, BF16, F64 };
+
+struct TensorView {
+  DType dtype;
+  std::vector<int64_t> shape;
+  const uint8_t* data = nullptr;
+  size_t nbytes = 0;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t s : shape) n *= s;
+    return n;
+  }
+};
+
+class SafeTensors {
+ public:
+  // `bytes` must outlive this object (it is the caller's buffer or mmap).
+  SafeTensors(const uint8_t* bytes, size_t len, const std::string& what);
+
+  bool has(const std::string& name) const { return map_.count(name) != 0; }
+  const TensorView& get(const std::string& name) const;
+  std::vector<std::string> names() const;
+
+  // Element values converted to f32, checked against the expected shape.
+  std::vector<float> to_f32(const std::string& name, const std::vector<int64_t>& want_shape) const;
+
+ private:
+  std::string what_;
+  std::unordered_map<std::string, TensorView> map_;
+};
+
+// One tensor to write: name, shape and bf16 payload.
+struct OutTensor {
+  std::string name;
+  std::vector<int64_t> shape;
+  std::vector<uint16_t> bf16;
+};
+
+// Serialise bf16 tensors into safetensors bytes.
+std::vector<uint8_t> write_safetensors_bf16(const std::vector<OutTensor>& ts);
+
+}  // namespace s1

@@ -1,0 +1,218 @@
+"""Synthetic requests and model configurations for the encoder-forward workloads.
+
+Rows follow ``build_sequence`` (runtime/crates/laya-core/src/sequence.rs:43-96):
+``[CLS] head_ids [SEP] ([MASK] opt_ids)* [SEP] state [SEP]``, and batches follow ``collate_to``
+(sequence.rs:132-166): rows right-padded with the pad id. Token ids are drawn uniformly from
+[0, 50280) by a seeded generator; there is no tokenizer in this path (the head text
+"<type> question: <instructions>" is stood in for by random ids of the same length).
+
+Workloads (ModernBERT-large shape, batch sizes as below):
+  * ``state128_1q``:  128-token state, 1 noul question, ~20 instruction ids (about 170 tokens).
+  * ``state512_1q``:  512-token state, 1 choice question with 3 labels (about 563 tokens).
+  * ``state512_10q``: 512-token state, 10 questions (4 choice with 3-5 labels, 3 score with 4
+    levels, 3 noul), instructions 10-30 ids; 10 rows of about 555-590 tokens.
+  * ``sweep64``: 64 requests with states of 128-2048 tokens, 3 questions each (192 rows).
+  * ``state8192_1q``: one 8192-token state (rows cut to max_len = 8192).
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass, field
+
+import numpy as np
+
+CLS, SEP, PAD, MASK = 50281, 50282, 50283, 50284
+RANDOM_ID_HIGH = 50280
+
+# encoder/config.json of ModernBERT-large (transformers 5.x layout, as the reference reads it:
+# runtime/crates/laya-core/src/config.rs:96-159).
+MODERNBERT_LARGE = {
+    "model_type": "modernbert",
+    "vocab_size": 50368,
+    "hidden_size": 1024,
+    "num_hidden_layers": 28,
+    "num_attention_heads": 16,
+    "intermediate_size": 2624,
+    "norm_eps": 1e-5,
+    "global_attn_every_n_layers": 3,
+    "local_attention": 128,
+    "rope_parameters": {
+        "full_attention": {"rope_type": "default", "rope_theta": 160000.0},
+        "sliding_attention": {"rope_type": "default", "rope_theta": 10000.0},
+    },
+    "pad_token_id": PAD,
+    "cls_token_id": CLS,
+    "sep_token_id": SEP,
+    "max_position_embeddings": 8192,
+}
+
+# rl_agent_config.json fields the backend reads (config.rs:9-40).
+AGENT = {
+    "encoder": "answerdotai/ModernBERT-large",
+    "head_layers": 2,
+    "max_len": 1024,
+    "head_max_len": 192,
+    "temperature": [1.0, 1.0, 1.0],
+}
+
+SCORER_WIDTH = 1024
+N_ACT = 2
+QTYPES = {"choice": 0, "score": 1, "noul": 2}
+
+
+def encoder_json(cfg: dict | None = None) -> str:
+    return json.dumps(cfg or MODERNBERT_LARGE)
+
+
+def agent_json(cfg: dict | None = None) -> str:
+    return json.dumps(cfg or AGENT)
+
+
+@dataclass
+class Batch:
+    """laya_core::Batch (runtime/crates/laya-core/src/backend.rs:72-98), row-major."""
+
+    n: int
+    len: int
+    kmax: int
+    input_ids: np.ndarray  # u32 [n*len]
+    attention_mask: np.ndarray  # u32 [n*len]
+    seq_lens: np.ndarray  # u64 [n]
+    marker_pos: np.ndarray  # u32 [n*kmax]
+    marker_count: np.ndarray  # u64 [n]
+    qtype: np.ndarray  # u32 [n]
+
+    def total_tokens(self) -> int:
+        return int(self.seq_lens.sum())
+
+    def rows(self, idx) -> "Batch":
+        """The sub-batch of rows `idx`, padded to the same `len` and `kmax`."""
+        idx = list(idx)
+        L, K = self.len, self.kmax
+        ids = self.input_ids.reshape(self.n, L)[idx].reshape(-1)
+        am = self.attention_mask.reshape(self.n, L)[idx].reshape(-1)
+        mp = self.marker_pos.reshape(self.n, K)[idx].reshape(-1) if K else self.marker_pos
+        return Batch(len(idx), L, K, np.ascontiguousarray(ids), np.ascontiguousarray(am),
+                     np.ascontiguousarray(self.seq_lens[idx]), np.ascontiguousarray(mp),
+                     np.ascontiguousarray(self.marker_count[idx]), np.ascontiguousarray(self.qtype[idx]))
+
+
+@dataclass
+class Question:
+    qtype: str
+    head_ids: list  # "<type> question: <instructions>" as ids
+    options: list = field(default_factory=list)  # list of id lists (without the [MASK])
+
+
+def build_sequence(state_ids, truncate_left: bool, q: Question, max_len: int, head_max_len: int):
+    """sequence.rs:43-96, over ids instead of text."""
+    head_ids = list(q.head_ids)
+    opt_ids = [[MASK] + list(o)[:48] for o in q.options]
+    total = sum(len(o) for o in opt_ids)
+    opt_budget = head_max_len - total
+    if opt_budget < 16:
+        per = max((head_max_len - 16) // max(len(opt_ids), 1), 4)
+        opt_ids = [o[:per] for o in opt_ids]
+        total = sum(len(o) for o in opt_ids)
+        opt_budget = head_max_len - total
+    head_ids = head_ids[: max(opt_budget, 8)]
+    ids = [CLS] + head_ids + [SEP]
+    markers = []
+    for o in opt_ids:
+        markers.append(len(ids))
+        ids.extend(o)
+    ids.append(SEP)
+    room = max(max_len - len(ids) - 1, 0)
+    st = list(state_ids)
+    st = st[max(len(st) - room, 0):] if truncate_left else st[: min(room, len(st))]
+    ids.extend(st)
+    ids.append(SEP)
+    ids = ids[:max_len]
+    markers = [m for m in markers if m < max_len]
+    return ids, markers
+
+
+def collate(items, pad_id: int = PAD, min_len: int = 0) -> Batch:
+    """sequence.rs:132-166: right-pad rows with pad_id."""
+    n = len(items)
+    L = max([len(ids) for ids, _, _ in items] + [min_len, 0])
+    K = max([len(m) for _, m, _ in items] + [0])
+    input_ids = np.full(n * L, pad_id, dtype=np.uint32)
+    mask = np.zeros(n * L, dtype=np.uint32)
+    mpos = np.zeros(n * K, dtype=np.uint32)
+    seq_lens = np.zeros(n, dtype=np.uint64)
+    mcount = np.zeros(n, dtype=np.uint64)
+    qtype = np.zeros(n, dtype=np.uint32)
+    for i, (ids, markers, qt) in enumerate(items):
+        input_ids[i * L: i * L + len(ids)] = ids
+        mask[i * L: i * L + len(ids)] = 1
+        mpos[i * K: i * K + len(markers)] = markers
+        seq_lens[i] = len(ids)
+        mcount[i] = len(markers)
+        qtype[i] = QTYPES[qt] if isinstance(qt, str) else qt
+    return Batch(n, L, K, input_ids, mask, seq_lens, mpos, mcount, qtype)
+
+
+def _ids(rng, n):
+    return rng.integers(0, RANDOM_ID_HIGH, size=int(n)).tolist()
+
+
+def _question(rng, qtype: str, n_instr: int, n_opts: int) -> Question:
+    prefix = 3  # "<type> question:" in the real tokenizer
+    opts = [_ids(rng, int(rng.integers(6, 11))) for _ in range(n_opts)]
+    return Question(qtype, _ids(rng, prefix + n_instr), opts)
+
+
+def request_rows(rng, state_len: int, questions, max_len: int, head_max_len: int):
+    state = _ids(rng, state_len)
+    items = []
+    for q in questions:
+        ids, markers = build_sequence(state, False, q, max_len, head_max_len)
+        items.append((ids, markers, q.qtype))
+    return items
+
+
+def workload(name: str, seed: int = 0, agent: dict | None = None) -> Batch:
+    """A seeded synthetic batch for one of the named workloads."""
+    agent = agent or AGENT
+    max_len, hml = agent["max_len"], agent["head_max_len"]
+    rng = np.random.default_rng(seed)
+    if name == "state128_1q":
+        qs = [_question(rng, "noul", 20, 2)]
+        return collate(request_rows(rng, 128, qs, max_len, hml))
+    if name == "state512_1q":
+        qs = [_question(rng, "choice", 20, 3)]
+        return collate(request_rows(rng, 512, qs, max_len, hml))
+    if name == "state512_10q":
+        qs = []
+        for _ in range(4):
+            qs.append(_question(rng, "choice", int(rng.integers(10, 31)), int(rng.integers(3, 6))))
+        for _ in range(3):
+            qs.append(_question(rng, "score", int(rng.integers(10, 31)), 4))
+        for _ in range(3):
+            qs.append(_question(rng, "noul", int(rng.integers(10, 31)), 2))
+        return collate(request_rows(rng, 512, qs, max_len, hml))
+    if name == "sweep64":
+        items = []
+        for _ in range(64):
+            L = int(rng.integers(128, 2049))
+            kinds = ["choice", "score", "noul"]
+            qs = [_question(rng, kinds[j], int(rng.integers(10, 31)), [3, 4, 2][j]) for j in range(3)]
+            items.extend(request_rows(rng, L, qs, 8192, hml))
+        return collate(items)
+    if name == "state8192_1q":
+        qs = [_question(rng, "choice", 20, 3)]
+        return collate(request_rows(rng, 8192, qs, 8192, hml))
+    raise KeyError(name)
+
+
+WORKLOADS = ["state128_1q", "state512_1q", "state512_10q", "sweep64", "state8192_1q"]
+
+
+def small_config(layers: int = 4, d: int = 512, heads: int = 8, inter: int = 384, local_attention: int = 32,
+                 vocab: int = 50368) -> dict:
+    """A reduced encoder of the same family (for fast tests)."""
+    c = dict(MODERNBERT_LARGE)
+    c.update(num_hidden_layers=layers, hidden_size=d, num_attention_heads=heads, intermediate_size=inter,
+             local_attention=local_attention, vocab_size=vocab)
+    return c

@@ -1,0 +1,170 @@
+"""Write the golden fixtures that pin the oracle.
+
+The expected values come from an implementation independent of both this repository and the
+reference: transformers' ModernBertModel (the same ModernBERT encoder; GeGLU `chunk(2)`,
+`rotate_half` RoPE, bidirectional sliding window) and torch's nn.TransformerEncoderLayer
+(norm_first, ReLU) for the decision head, with a LayerNorm -> Linear -> GELU -> Linear scorer,
+all in float32 on the CPU. The weights are the synthetic checkpoint of libsys1hip's
+s1_synth_checkpoint, so the fixture only stores the seed, the batch and the outputs.
+
+Run here (it needs transformers and a built libsys1hip.so):
+    python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT))
+
+from sys1rust_amd.backend import synth_checkpoint  # noqa: E402
+from sys1rust_amd.workloads import MODERNBERT_LARGE, collate  # noqa: E402
+
+OUT = Path(__file__).resolve().parent
+
+
+def load_bf16(st: bytes) -> dict:
+    import struct
+
+    (hl,) = struct.unpack("<Q", st[:8])
+    hdr = json.loads(st[8: 8 + hl])
+    out = {}
+    for k, t in hdr.items():
+        if k == "__metadata__":
+            continue
+        s, e = t["data_offsets"]
+        u = np.frombuffer(st[8 + hl + s: 8 + hl + e], dtype=np.uint16).astype(np.uint32) << 16
+        out[k] = torch.from_numpy(u.view(np.float32).reshape(t["shape"]).copy())
+    return out
+
+
+def hf_encoder(cfg: dict, w: dict):
+    from transformers import ModernBertConfig, ModernBertModel
+
+    hc = ModernBertConfig(
+        vocab_size=cfg["vocab_size"], hidden_size=cfg["hidden_size"], num_hidden_layers=cfg["num_hidden_layers"],
+        num_attention_heads=cfg["num_attention_heads"], intermediate_size=cfg["intermediate_size"],
+        norm_eps=cfg["norm_eps"], global_attn_every_n_layers=cfg["global_attn_every_n_layers"],
+        local_attention=cfg["local_attention"], rope_parameters=json.loads(json.dumps(cfg["rope_parameters"])),
+        pad_token_id=cfg["pad_token_id"], max_position_embeddings=cfg["max_position_embeddings"],
+        attention_bias=False, mlp_bias=False, norm_bias=False, hidden_activation="gelu",
+        embedding_dropout=0.0, attention_dropout=0.0, mlp_dropout=0.0,
+    )
+    hc._attn_implementation = "eager"
+    m = ModernBertModel(hc).eval().float()
+    sd = {k[len("encoder."):]: v for k, v in w.items() if k.startswith("encoder.")}
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected, unexpected
+    assert all("rotary" in k or "inv_freq" in k for k in missing), missing
+    # The window rule the reference uses: query i sees key j iff |i - j| <= local_attention / 2
+    # (runtime/crates/laya-mlx/src/lib.rs:514-523, config.rs:73-74).
+    from transformers.masking_utils import sliding_window_bidirectional_overlay
+
+    f = sliding_window_bidirectional_overlay(hc.sliding_window)
+    W = cfg["local_attention"] // 2
+    for i in range(0, 3 * W):
+        for j in range(0, 3 * W):
+            assert bool(f(0, 0, i, j)) == (abs(i - j) <= W), (i, j)
+    th = {t: hc.rope_parameters[t]["rope_theta"] for t in ("full_attention", "sliding_attention")}
+    assert th["full_attention"] == cfg["rope_parameters"]["full_attention"]["rope_theta"]
+    assert th["sliding_attention"] == cfg["rope_parameters"]["sliding_attention"]["rope_theta"]
+    for i, lt in enumerate(hc.layer_types):
+        assert (lt == "sliding_attention") == (i % cfg["global_attn_every_n_layers"] != 0)
+    return m
+
+
+def head_and_scorer(d: int, head_layers: int, w: dict):
+    layers = []
+    for j in range(head_layers):
+        L = torch.nn.TransformerEncoderLayer(d, nhead=max(1, d // 64), dim_feedforward=4 * d, dropout=0.0,
+                                             activation="relu", batch_first=True, norm_first=True)
+        p = f"head.layers.{j}."
+        sd = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
+        L.load_state_dict(sd)
+        layers.append(L.eval())
+    S = w["scorer.1.weight"].shape[0]
+    scorer = torch.nn.Sequential(torch.nn.LayerNorm(d), torch.nn.Linear(d, S), torch.nn.GELU(), torch.nn.Linear(S, 1))
+    scorer.load_state_dict({k[len("scorer."):]: v for k, v in w.items() if k.startswith("scorer.")})
+    return layers, scorer.eval()
+
+
+@torch.no_grad()
+def reference_outputs(cfg: dict, agent: dict, seed: int, batch, scorer_width: int):
+    st = synth_checkpoint(json.dumps(cfg), json.dumps(agent), seed, scorer_width=scorer_width, n_act=2, jitter=True)
+    w = load_bf16(st)
+    enc = hf_encoder(cfg, w)
+    n, L, K = batch.n, batch.len, batch.kmax
+    ids = torch.from_numpy(batch.input_ids.reshape(n, L).astype(np.int64))
+    am = torch.from_numpy(batch.attention_mask.reshape(n, L).astype(np.int64))
+    hidden = enc(input_ids=ids, attention_mask=am).last_hidden_state.float()
+    layers, scorer = head_and_scorer(cfg["hidden_size"], agent["head_layers"], w)
+    h = hidden + w["type_emb.weight"][torch.from_numpy(batch.qtype.astype(np.int64))][:, None, :]
+    # Run the head without torch's fast path so that padded keys are masked additively as in
+    # the reference (only real positions are compared).
+    kpm = am == 0
+    for Lyr in layers:
+        x = Lyr.norm1(h)
+        a, _ = Lyr.self_attn(x, x, x, key_padding_mask=kpm, need_weights=False)
+        h = h + a
+        h = h + Lyr.linear2(torch.relu(Lyr.linear1(Lyr.norm2(h))))
+    mp = torch.from_numpy(batch.marker_pos.reshape(n, K).astype(np.int64))
+    rows = torch.gather(h, 1, mp[:, :, None].expand(n, K, h.shape[-1]))
+    logits = scorer(rows).reshape(n, K)
+    mc = torch.from_numpy(batch.marker_count.astype(np.int64))
+    logits = torch.where(torch.arange(K)[None, :] < mc[:, None], logits, torch.tensor(-1e4))
+    pooled = h[:, 0, :]
+    return hidden.numpy(), logits.reshape(-1).numpy(), pooled.reshape(-1).numpy()
+
+
+def small_case():
+    cfg = dict(MODERNBERT_LARGE)
+    cfg.update(vocab_size=1024, hidden_size=512, num_hidden_layers=4, num_attention_heads=8, intermediate_size=384,
+               local_attention=32, pad_token_id=1002)
+    agent = {"head_layers": 2, "max_len": 512, "head_max_len": 192}
+    rng = np.random.default_rng(7)
+    items = []
+    for L, K, qt in [(40, 3, 0), (57, 4, 1), (23, 2, 2)]:
+        ids = [1000] + rng.integers(0, 1000, L - 2).tolist() + [1001]
+        markers = sorted(rng.choice(np.arange(2, L - 2), size=K, replace=False).tolist())
+        items.append((ids, markers, qt))
+    return cfg, agent, collate(items, pad_id=cfg["pad_token_id"])
+
+
+def full_case():
+    cfg = dict(MODERNBERT_LARGE)
+    agent = {"head_layers": 2, "max_len": 1024, "head_max_len": 192}
+    rng = np.random.default_rng(11)
+    L = 150
+    ids = [50281] + rng.integers(0, 50280, L - 2).tolist() + [50282]
+    items = [(ids, [24, 33], 2)]
+    return cfg, agent, collate(items)
+
+
+def write(name: str, cfg, agent, batch, seed: int, scorer_width: int, token_stride: int):
+    hidden, logits, pooled = reference_outputs(cfg, agent, seed, batch, scorer_width)
+    am = batch.attention_mask.reshape(batch.n, batch.len)
+    # Real tokens only (every `token_stride`-th of them to keep the file small).
+    sel = [(r, p) for r in range(batch.n) for p in range(batch.len) if am[r, p] == 1 and p % token_stride == 0]
+    sel = np.array(sel, dtype=np.int32)
+    np.savez_compressed(
+        OUT / f"{name}.npz",
+        encoder_config=json.dumps(cfg), agent_config=json.dumps(agent), seed=seed, scorer_width=scorer_width,
+        n=batch.n, len=batch.len, kmax=batch.kmax, input_ids=batch.input_ids, attention_mask=batch.attention_mask,
+        seq_lens=batch.seq_lens, marker_pos=batch.marker_pos, marker_count=batch.marker_count, qtype=batch.qtype,
+        hidden_sel=sel, hidden=hidden[sel[:, 0], sel[:, 1]].astype(np.float32), logits=logits.astype(np.float32),
+        pooled=pooled.astype(np.float32),
+        source=f"transformers {__import__('transformers').__version__} ModernBertModel + torch {torch.__version__} "
+               f"TransformerEncoderLayer, float32 CPU",
+    )
+    print(name, "hidden", hidden.shape, "logits", logits[:6])
+
+
+if __name__ == "__main__":
+    torch.manual_seed(0)
+    write("golden_small", *small_case(), seed=1234, scorer_width=256, token_stride=1)
+    write("golden_large", *full_case(), seed=4321, scorer_width=1024, token_stride=5)

@@ -1,0 +1,227 @@
+"""Kernel-level parity on the GPU, through the C ABI's s1k_* entry points.
+
+GEMM epilogues are checked against a float32 torch product of the same bf16 operands; the fused
+Wqkv + split + RoPE product (the isolated M=512, K=1024, N=3072 case at both RoPE bases), the
+standalone split + RoPE pass, attention and LayerNorm against the oracle's formulas in float32.
+Tolerances are bf16-output tolerances: the kernels accumulate in f32 and round once to bf16
+(relative step 2^-8).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from sys1rust_amd import _lib as L
+
+    return L
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    return torch.device("cuda:0")
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def bf16_bits(t):
+    return t.to(torch.bfloat16).contiguous().view(torch.int16)
+
+
+def gemm(A, W, M, N, K, epi=0, act=0, bias=None, C_out=None):
+    L = _lib()
+    dev = A.device
+    if C_out is None:
+        if epi in (1, 3):
+            C_out = torch.zeros(M, N, dtype=torch.float32, device=dev)
+        elif epi == 2:
+            C_out = torch.zeros(M, N // 2, dtype=torch.int16, device=dev)
+        else:
+            C_out = torch.zeros(M, N, dtype=torch.int16, device=dev)
+    ldc = C_out.shape[1]
+    L.check(L.lib().s1k_gemm(ptr(A), K, ptr(W), K, ptr(C_out), ldc, ptr(bias) if bias is not None else None, M, N, K,
+                             epi, act, stream()))
+    torch.cuda.synchronize()
+    return C_out
+
+
+def as_f32(bits):
+    return bits.view(torch.bfloat16).float()
+
+
+SHAPES = [(1, 128, 64), (37, 256, 128), (170, 3072, 1024), (257, 1024, 1024), (563, 1024, 2624), (600, 5248, 1024),
+          (1000, 4096, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_f32_and_bf16_outputs(dev, M, N, K):
+    say(f"gemm M={M} N={N} K={K}")
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N)
+    A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
+    W = bf16_bits(torch.randn(N, K, generator=g) * 0.02).to(dev)
+    ref = as_f32(A) @ as_f32(W).T
+    out = gemm(A, W, M, N, K, epi=3)
+    scale = float(ref.abs().max())
+    err = float((out - ref).abs().max())
+    assert err <= 2e-5 * scale + 1e-6, (err, scale)
+    ob = as_f32(gemm(A, W, M, N, K, epi=0))
+    err = (ob - ref).abs()
+    assert bool((err <= ref.abs() * 2 ** -8 + 1e-5 * scale).all()), float(err.max())
+
+
+def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev):
+    M, N, K = 300, 1024, 512
+    g = torch.Generator(device="cpu").manual_seed(5)
+    A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
+    W = bf16_bits(torch.randn(N, K, generator=g) * 0.05).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.1).to(dev)
+    ref = as_f32(A) @ as_f32(W).T + bias
+    for act, f in [(1, torch.relu), (2, lambda x: torch.nn.functional.gelu(x))]:
+        say(f"epilogue act={act}")
+        ob = as_f32(gemm(A, W, M, N, K, epi=0, act=act, bias=bias))
+        r = f(ref)
+        assert bool(((ob - r).abs() <= r.abs() * 2 ** -8 + 1e-4).all())
+    say("epilogue residual")
+    h0 = torch.randn(M, N, generator=g).to(dev)
+    h = h0.clone()
+    gemm(A, W, M, N, K, epi=1, bias=bias, C_out=h)
+    assert float((h - (h0 + ref)).abs().max()) < 1e-4
+    say("epilogue geglu")
+    # Wi = [x rows | gate rows]; the kernel wants them interleaved by blocks of 32 rows.
+    I = N // 2
+    Wf = as_f32(W)
+    Wi = torch.cat([Wf[:I].reshape(I // 32, 32, K), Wf[I:].reshape(I // 32, 32, K)], dim=1).reshape(N, K)
+    Wi_bits = bf16_bits(Wi)
+    act = as_f32(gemm(A, Wi_bits, M, N, K, epi=2))
+    x = as_f32(A) @ Wf[:I].T
+    gate = as_f32(A) @ Wf[I:].T
+    r = torch.nn.functional.gelu(x) * gate
+    assert bool(((act - r).abs() <= r.abs() * 2 ** -7 + 1e-4).all()), float((act - r).abs().max())
+
+
+@pytest.mark.parametrize("theta", [160000.0, 10000.0])
+def test_fused_wqkv_split_rope_m512(dev, theta):
+    """Isolated fused Wqkv GEMM + split + RoPE: M=512, K=1024, N=3072, A ~ N(0,1), W ~ N(0,0.02),
+    positions 0..511."""
+    say(f"qkv_rope theta={theta}")
+    M, d = 512, 1024
+    g = torch.Generator(device="cpu").manual_seed(int(theta) % 97)
+    A = bf16_bits(torch.randn(M, d, generator=g)).to(dev)
+    W = bf16_bits(torch.randn(3 * d, d, generator=g) * 0.02).to(dev)
+    pos = torch.arange(M, dtype=torch.int32, device=dev)
+    q, k, v = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(3))
+    L = _lib()
+    L.check(L.lib().s1k_qkv_rope(ptr(A), ptr(W), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(v), stream()))
+    torch.cuda.synchronize()
+    qkv = (as_f32(A) @ as_f32(W).T).cpu().numpy()
+    cos, sin = O.rope_tables(theta, M, 64)
+    want = []
+    for part in range(3):
+        x = qkv[:, part * d:(part + 1) * d].reshape(M, 16, 64).transpose(1, 0, 2)
+        want.append(O.rope(x, cos, sin) if part < 2 else x)
+    for got, ref in zip((q, k, v), want):
+        g_ = as_f32(got).cpu().numpy()
+        err = np.abs(g_ - ref)
+        assert np.all(err <= np.abs(ref) * 2 ** -8 + 2e-4), float(err.max())
+
+
+@pytest.mark.parametrize("theta", [160000.0, 10000.0, 0.0])
+def test_split_rope_pass(dev, theta):
+    say(f"split_rope theta={theta}")
+    M, d = 700, 1024
+    g = torch.Generator(device="cpu").manual_seed(3)
+    qkv = bf16_bits(torch.randn(M, 3 * d, generator=g)).to(dev)
+    pos = torch.arange(M, dtype=torch.int32, device=dev) * 11  # positions up to 7689
+    q, k, v = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(3))
+    L = _lib()
+    L.check(L.lib().s1k_split_rope(ptr(qkv), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(v), stream()))
+    torch.cuda.synchronize()
+    x = as_f32(qkv).cpu().numpy()
+    p = pos.cpu().numpy()
+    for part, got in enumerate((q, k, v)):
+        ref = x[:, part * d:(part + 1) * d].reshape(M, 16, 64).transpose(1, 0, 2)
+        if part < 2 and theta > 0:
+            cos, sin = O.rope_tables(theta, int(p.max()) + 1, 64)
+            c, s = cos[p], sin[p]
+            ref = np.concatenate([ref[..., :32] * c - ref[..., 32:] * s, ref[..., :32] * s + ref[..., 32:] * c], -1)
+        g_ = as_f32(got).cpu().numpy()
+        if part == 2 or theta == 0:
+            assert np.array_equal(g_, ref)  # an exact copy
+        else:
+            assert np.all(np.abs(g_ - ref) <= np.abs(ref) * 2 ** -8 + 1e-6)
+
+
+def attention_ref(q, k, v, starts, window, scale):
+    """float32 per-row softmax(q k^T scale) v with the row and window masks."""
+    H, T, _ = q.shape
+    out = torch.zeros(T, H * 64, dtype=torch.float32)
+    for r in range(len(starts) - 1):
+        a, b = starts[r], starts[r + 1]
+        qq, kk, vv = q[:, a:b], k[:, a:b], v[:, a:b]
+        s = (qq @ kk.transpose(1, 2)) * scale
+        if window >= 0:
+            i = torch.arange(b - a)
+            s = s.masked_fill((i[:, None] - i[None, :]).abs() > window, float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out[a:b] = (p @ vv).transpose(0, 1).reshape(b - a, H * 64)
+    return out
+
+
+@pytest.mark.parametrize("window", [-1, 64])
+@pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048]])
+def test_attention_varlen(dev, window, lens):
+    say(f"attention window={window} lens={lens}")
+    H = 16
+    starts = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(starts[-1])
+    g = torch.Generator(device="cpu").manual_seed(T + window)
+    q, k, v = (torch.randn(H, T, 64, generator=g) for _ in range(3))
+    qb, kb, vb = (bf16_bits(x).to(dev) for x in (q, k, v))
+    out = torch.zeros(T, H * 64, dtype=torch.int16, device=dev)
+    L = _lib()
+    st = np.ascontiguousarray(starts)
+    L.check(L.lib().s1k_attention(ptr(qb), ptr(kb), ptr(vb), T, H, st.ctypes.data_as(L.i32p), len(lens), window,
+                                  0.125, ptr(out), stream()))
+    torch.cuda.synchronize()
+    ref = attention_ref(as_f32(qb.cpu()), as_f32(kb.cpu()), as_f32(vb.cpu()), starts.tolist(), window, 0.125)
+    got = as_f32(out.cpu())
+    # P is rounded to bf16 before the PV product: allow ~2^-8 relative on each term
+    err = (got - ref).abs()
+    assert float(err.max()) <= 2e-2, float(err.max())
+    assert float(err.mean()) <= 2e-3, float(err.mean())
+
+
+def test_layernorm(dev):
+    say("layernorm")
+    M, d = 333, 1024
+    g = torch.Generator(device="cpu").manual_seed(9)
+    x = (torch.randn(M, d, generator=g) * 3 + 0.5).to(dev)
+    w = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    b = (0.1 * torch.randn(d, generator=g)).to(dev)
+    y = torch.zeros(M, d, dtype=torch.int16, device=dev)
+    L = _lib()
+    L.check(L.lib().s1k_layernorm(ptr(x), ptr(w), ptr(b), 1e-5, M, d, ptr(y), stream()))
+    torch.cuda.synchronize()
+    ref = O.layer_norm(x.cpu().numpy(), w.cpu().numpy(), b.cpu().numpy(), 1e-5)
+    got = as_f32(y).cpu().numpy()
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -8 + 1e-5)
