@@ -54,6 +54,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload the CPU baseline runs")
     ap.add_argument("--settings", default="")
+    ap.add_argument("--no-context", action="store_true",
+                    help="time only the headline workload (no 1-question shapes), e.g. under a profiler")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -70,13 +72,12 @@ def main() -> int:
     enc_json, agent_json = json.dumps(MODERNBERT_LARGE), json.dumps(AGENT)
     t0 = time.time()
     ckpt = synth_checkpoint(enc_json, agent_json, seed=args.seed, scorer_width=SCORER_WIDTH)
-    settings = ",".join(x for x in ["ops", args.settings] if x)
-    model = HipBackend(ckpt, enc_json, agent_json, settings=settings)
+    model = HipBackend(ckpt, enc_json, agent_json, settings=args.settings)
     model.warmup()
     print(f"[bench] model ready in {time.time() - t0:.1f}s: {model.name()} {model.active_kernels()}",
           file=sys.stderr, flush=True)
 
-    def run(b, steps, warmup):
+    def run(b, steps, warmup, model=model):
         for _ in range(warmup):
             out = model.forward(b)
             decode_answers(out.logits, b.kmax, b.marker_count, b.qtype)
@@ -92,15 +93,22 @@ def main() -> int:
     # Context shapes (1 question at 128 and 512 tokens), then the headline workload last so its
     # per-kernel statistics are the ones reported.
     shapes = {}
-    for name in ["state128_1q", "state512_1q"]:
+    for name in ([] if args.no_context else ["state128_1q", "state512_1q"]):
         b = workload(name, seed=args.seed)
         ms, _ = run(b, max(5, args.steps // 2), args.warmup)
         shapes[name] = round(ms, 4)
         print(f"[bench] {name}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
     b = workload(args.workload, seed=args.seed)
-    ms, stats = run(b, args.steps, args.warmup)
+    ms, _ = run(b, args.steps, args.warmup)
     shapes[args.workload] = round(ms, 4)
     print(f"[bench] {args.workload}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
+
+    # Kernel timing: the same steps on a second instance with the `ops` setting, which records a
+    # HIP event pair around every launch on the model's stream (and so runs without graphs).
+    kmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in ["ops", args.settings] if x))
+    ms_eager, stats = run(b, args.steps, args.warmup, model=kmodel)
+    kmodel.close()
+    print(f"[bench] {args.workload}: {ms_eager:.3f} ms/request with per-kernel events", file=sys.stderr, flush=True)
 
     T = b.total_tokens()
     d, I = MODERNBERT_LARGE["hidden_size"], MODERNBERT_LARGE["intermediate_size"]
@@ -130,6 +138,8 @@ def main() -> int:
         "flop_per_launch": gemm_flops(dom, T, P, R, d, I, SCORER_WIDTH),
         "avg_launch_us": dk["avg_us"],
         "all_encoder_gemms_tflops": round(gemm_flop_step / (gemm_ms_step * 1e-3) / 1e12, 1),
+        "measured": f"HIP events around every launch on the model's stream over {args.steps} steps of the "
+                    f"workload ({ms_eager:.3f} ms/request in that region)",
     }
 
     cpu = None

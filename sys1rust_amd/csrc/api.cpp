@@ -1,6 +1,6 @@
 // The C ABI of libsys1hip (include/sys1hip.h). Every entry point catches all exceptions and
 // turns them into an error kind plus a thread-local message; nothing aborts.
-#include "../../include/sys1hip.h"
+#include "sys1hip.h"
 
 #include <fstream>
 #include <memory>
@@ -203,6 +203,35 @@ void s1_op_stats_reset(s1_model* h) {
   if (h && h->m) h->m->stats.clear();
 }
 
+}  // extern "C"
+
+namespace {
+
+// Split-K workspace of the kernel-level entry points: grown on demand, kept for the thread.
+struct Workspace {
+  float* p = nullptr;
+  size_t floats = 0;
+};
+thread_local Workspace g_ws;
+
+float* workspace(size_t floats, hipStream_t st) {
+  if (floats == 0) return nullptr;
+  if (floats > g_ws.floats) {
+    if (g_ws.p) {
+      hip_ok(hipStreamSynchronize(st), "sync");
+      hip_ok(hipFree(g_ws.p), "hipFree");
+      g_ws.p = nullptr;
+    }
+    hip_ok(hipMalloc(&g_ws.p, floats * 4), "hipMalloc(workspace)");
+    g_ws.floats = floats;
+  }
+  return g_ws.p;
+}
+
+}  // namespace
+
+extern "C" {
+
 int s1k_gemm(const void* A, int lda, const void* W, int ldw, void* C, int ldc, const float* bias, int M, int N, int K,
              int epi, int act, void* stream) {
   return guard([&] {
@@ -221,9 +250,13 @@ int s1k_gemm(const void* A, int lda, const void* W, int ldw, void* C, int ldc, c
     g.ldc = ldc;
     g.epi = epi;
     g.act = act;
-    if (const char* e = s1::gemm_check(g)) s1::fail(s1::kConfig, e);
     if (!A || !W || !C) s1::fail(s1::kConfig, "s1k_gemm: NULL buffer");
-    s1::gemm_launch(g, static_cast<hipStream_t>(stream));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const s1::GemmPlan gp = s1::gemm_plan(M, N, K);
+    g.splits = gp.splits;
+    g.ws = workspace(gp.ws_floats, st);
+    if (const char* e = s1::gemm_check(g)) s1::fail(s1::kConfig, e);
+    s1::gemm_launch(g, st);
     hip_ok(hipGetLastError(), "s1k_gemm launch");
   });
 }
@@ -304,6 +337,9 @@ int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos,
     g.rope_sin = g_rope.s;
     g.rope_T = M;
     g.rope_d = d;
+    const s1::GemmPlan gp = s1::gemm_plan(M, 3 * d, d);
+    g.splits = gp.splits;
+    g.ws = workspace(gp.ws_floats, st);
     if (const char* e = s1::gemm_check(g)) s1::fail(s1::kConfig, e);
     s1::gemm_launch(g, st);
     hip_ok(hipGetLastError(), "s1k_qkv_rope launch");

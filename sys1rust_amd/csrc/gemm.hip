@@ -22,6 +22,8 @@
 //   EPI_F32    C f32 = acc (+ bias)
 //   EPI_ROPE   the encoder's Wqkv: split into q|k|v, RoPE on q and k (cos/sin table by token
 //              position), written head-major as [H, T, 64] bf16 each
+#include <algorithm>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -30,59 +32,100 @@ namespace s1 {
 namespace {
 
 constexpr int BK = 64;
-constexpr int LDK = BK + 8;  // padded LDS row, in bf16 elements (144 bytes)
 
-template <int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
-  constexpr int NT = WM * WN * 64;
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads: the fence would make the compiler
+// drain every outstanding global->LDS load (vmcnt(0)) at each k-tile and serialise the pipeline.
+// The "memory" clobber keeps LDS accesses on their side of it; completion of the async loads is
+// awaited explicitly with wait_vmcnt before it.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_barrier" ::: "memory"); }
+
+// Wait until at most `ahead` k-tiles of this wave's loads (LPW loads each) are in flight.
+template <int LPW, int MAXA>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+  if constexpr (MAXA > 0) {
+    if (ahead >= MAXA) {
+      wait_vmcnt<MAXA * LPW>();
+      return;
+    }
+    wait_ahead<LPW, MAXA - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+  constexpr int NW = WM * WN;                // waves; each owns a TM x TN sub-tile
   constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 32, FN = TN / 32;
-  constexpr int A_CH = BM * BK / 8 / NT;
-  constexpr int W_CH = BN * BK / 8 / NT;
-  static_assert(A_CH * NT * 8 == BM * BK && W_CH * NT * 8 == BN * BK, "tile not divisible");
-  static_assert(EPI != EPI_GEGLU || (FN % 2) == 0, "geglu needs fragment pairs");
+  constexpr int FM = TM / 32, FN = TN / 32;  // 32 x 32 MFMA fragments per wave
+  constexpr int CH = BK / 8;                 // 16-byte chunks per LDS row
+  constexpr int ROWB = BK * 2;               // bytes per LDS row
+  constexpr int RG = 1024 / ROWB;            // rows per 1 KiB direct load
+  constexpr int AG = BM / RG, WG = BN / RG;  // direct loads per k-tile
+  constexpr int LPW = (AG + WG) / NW;        // loads per wave per k-tile
+  constexpr int A_BYTES = BM * ROWB, STAGE_BYTES = (BM + BN) * ROWB;
+  static_assert(FN % 2 == 0 && TN % 64 == 0, "epilogues pair the fragments of 64-column groups");
+  constexpr int SW = 16 / CH;                // rows sharing one 256-byte bank line
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(LPW * NW == AG + WG, "load groups must split evenly over the waves");
+  static_assert((STAGES - 2) * LPW < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sW[2][BN * LDK];
+  // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of ROWB bytes. The 16-byte chunk c
+  // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
+  // consecutive rows, the same k; 64 banks of 4 bytes) then hit 16 distinct 16-byte bank groups
+  // without padding, which the direct loads (whole 1 KiB runs) could not write.
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
+  // Tile order: each XCD takes a contiguous run of logical tiles (xcd_remap), and the run walks
+  // groups of GM row tiles across all column tiles, GM fastest. The ~32 workgroups an XCD holds
+  // at once then cover a GM x (32 / GM) patch, so its L2 serves every A row panel to many
+  // column tiles instead of re-reading the activations from HBM once per column tile.
+  constexpr int GM = BM >= 256 ? 4 : 8;
   const int mt = (g.M + BM - 1) / BM;
+  const int nt = g.N / BN;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile_m = bid % mt, tile_n = bid / mt;
+  const int grp = bid / (GM * nt);
+  const int gm = min(GM, mt - grp * GM);
+  const int loc = bid - grp * GM * nt;
+  const int tile_m = grp * GM + loc % gm, tile_n = loc / gm;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
-  const int KT = g.K / BK;
+  // This workgroup's k-tiles: [kt0, kt0 + NK) of the K / BK (split-K divides them evenly).
+  const int KT_ALL = g.K / BK;
+  const int split = blockIdx.y, S = gridDim.y;
+  const int kt0 = (split * KT_ALL) / S;
+  const int NK = ((split + 1) * KT_ALL) / S - kt0;
 
-  const uint16_t* __restrict__ A = g.A;
-  const uint16_t* __restrict__ W = g.W;
-
-  uint4 ra[A_CH], rw[W_CH];
-#define S1_GLOAD(kt)                                                                         \
-  do {                                                                                       \
-    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                       \
-      const int c = tid + i * NT;                                                            \
-      const int gr = min(m0 + (c >> 3), g.M - 1);                                            \
-      ra[i] = *reinterpret_cast<const uint4*>(A + size_t(gr) * g.lda + (kt) * BK + (c & 7) * 8); \
-    }                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < W_CH; ++i) {                                       \
-      const int c = tid + i * NT;                                                            \
-      rw[i] = *reinterpret_cast<const uint4*>(W + size_t(n0 + (c >> 3)) * g.ldw + (kt) * BK + (c & 7) * 8); \
-    }                                                                                        \
-  } while (0)
-#define S1_SSTORE(buf)                                                                       \
-  do {                                                                                       \
-    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                       \
-      const int c = tid + i * NT;                                                            \
-      *reinterpret_cast<uint4*>(&sA[buf][(c >> 3) * LDK + (c & 7) * 8]) = ra[i];             \
-    }                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < W_CH; ++i) {                                       \
-      const int c = tid + i * NT;                                                            \
-      *reinterpret_cast<uint4*>(&sW[buf][(c >> 3) * LDK + (c & 7) * 8]) = rw[i];             \
-    }                                                                                        \
-  } while (0)
+  // Global -> LDS without registers (global_load_lds_dwordx4): lane l of a load moves 16 bytes
+  // of row l / CH of its RG-row group, chunk (l % CH) ^ swizzle, into slot l % CH.
+  const int lrow = lane / CH, lslot = lane % CH;
+  auto issue = [&](int stage, int kt) {
+    char* sb = smem + stage * STAGE_BYTES;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int gi = wave + j * NW;
+      if (gi < AG) {
+        const int r = gi * RG + lrow;
+        const int c = lslot ^ ((r / SW) % CH);
+        const uint16_t* src = g.A + size_t(min(m0 + r, g.M - 1)) * g.lda + kt * BK + c * 8;
+        __builtin_amdgcn_global_load_lds(src, sb + gi * 1024, 16, 0, 0);
+      } else {
+        const int r = (gi - AG) * RG + lrow;
+        const int c = lslot ^ ((r / SW) % CH);
+        const uint16_t* src = g.W + size_t(n0 + r) * g.ldw + kt * BK + c * 8;
+        __builtin_amdgcn_global_load_lds(src, sb + A_BYTES + (gi - AG) * 1024, 16, 0, 0);
+      }
+    }
+  };
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -92,38 +135,61 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  S1_GLOAD(0);
-  S1_SSTORE(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < NK) issue(s, kt0 + s);
 
-  const int lrow = lane & 31;
-  const int lk = (lane >> 5) * 8;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    // The last iteration reloads its own tile into the idle buffer: harmless, and it keeps the
-    // staging registers free of control flow.
-    S1_GLOAD(min(kt + 1, KT - 1));
+  const int lr = lane & 31, lh = lane >> 5;
+  for (int it = 0; it < NK; ++it) {
+    // This wave's loads of k-tile `it` are done once at most `ahead` later k-tiles are in flight.
+    wait_ahead<LPW, STAGES - 2>(min(STAGES - 2, NK - 1 - it));
+    // Every wave's loads of `it` have landed, and every wave is done with k-tile it - 1, whose
+    // buffer the next issue overwrites.
+    barrier_lds();
+    if (it + STAGES - 1 < NK) issue((it + STAGES - 1) % STAGES, kt0 + it + STAGES - 1);
+    const char* sa = smem + (it % STAGES) * STAGE_BYTES;
+    const char* sw = sa + A_BYTES;
+    bf16x8 af[2][FM], bw[2][FN];
+    auto frag = [&](int ks, int buf) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * TM + i * 32 + lr;
+        af[buf][i] = *reinterpret_cast<const bf16x8*>(sa + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int row = wn * TN + j * 32 + lr;
+        bw[buf][j] = *reinterpret_cast<const bf16x8*>(sw + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
+      }
+    };
+    frag(0, 0);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[FM], bw[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * TM + i * 32 + lrow) * LDK + ks * 16 + lk]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bw[j] = *reinterpret_cast<const bf16x8*>(&sW[buf][(wn * TN + j * 32 + lrow) * LDK + ks * 16 + lk]);
+      if (ks + 1 < BK / 16) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bw[ks & 1][j], acc[i][j], 0, 0, 0);
     }
-    S1_SSTORE(buf ^ 1);
-    __syncthreads();
   }
 
-#undef S1_GLOAD
-#undef S1_SSTORE
+  if (S > 1) {
+    // Split-K: this k-range's partial tile goes to ws[split] as f32; splitk_epilogue_kernel
+    // sums the splits and applies the epilogue.
+    float* part = g.ws + size_t(split) * g.M * g.N;
+    const int lh2 = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + wm * TM + i * 32 + (e >> 2) * 8 + 4 * lh2 + (e & 3);
+          if (row < g.M) part[size_t(row) * g.N + n0 + wn * TN + j * 32 + (lane & 31)] = acc[i][j][e];
+        }
+    return;
+  }
 
   // Epilogue. Lane holds column (lane & 31) and rows 8q + 4h + r of each 32x32 fragment.
   const int h = lane >> 5;
@@ -208,22 +274,101 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
 void launch_t(const GemmArgs& g, hipStream_t st) {
   const int mt = (g.M + BM - 1) / BM, nt = g.N / BN;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI>), dim3(mt * nt), dim3(WM * WN * 64), 0, st, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, STAGES, WM, WN, EPI>), dim3(mt * nt, g.splits), dim3(WM * WN * 64), 0,
+                     st, g);
 }
 
 template <int EPI>
 void launch_e(const GemmArgs& g, hipStream_t st) {
-  // Small M: 64-row tiles so more workgroups stream the weight; otherwise 128 x 128.
-  if (g.M <= 256)
-    launch_t<64, 128, 2, 2, EPI>(g, st);
+  // 64-row tiles for tiny M; otherwise 128 x 128 with two k-tiles in LDS (64 KiB), which lets
+  // two workgroups share a CU (two waves per SIMD).
+  if (g.M <= 64)
+    launch_t<64, 128, 64, 2, 1, 2, EPI>(g, st);
   else
-    launch_t<128, 128, 2, 2, EPI>(g, st);
+    launch_t<128, 128, 64, 2, 2, 2, EPI>(g, st);
+}
+
+// Sum of the split-K partials in split order, then the GEMM's epilogue. One thread per row and
+// column pair (c, c + 32) of a 64-column group, the pair the GeGLU and RoPE epilogues combine.
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int half = g.N / 2;
+  if (gid >= (long long)g.M * half) return;
+  const int row = int(gid / half);
+  const int p = int(gid % half);
+  const int c1 = (p / 32) * 64 + (p % 32), c2 = c1 + 32;
+  float x1 = 0.0f, x2 = 0.0f;
+  for (int s = 0; s < g.splits; ++s) {
+    const float* part = g.ws + (size_t(s) * g.M + row) * g.N;
+    x1 += part[c1];
+    x2 += part[c2];
+  }
+  if (g.epi == EPI_GEGLU) {
+    uint16_t* C = reinterpret_cast<uint16_t*>(g.C);
+    C[size_t(row) * g.ldc + p] = f2bf(gelu_erf(x1) * x2);
+    return;
+  }
+  if (g.epi == EPI_ROPE) {
+    const int part = c1 / g.rope_d;
+    const int head = (c1 - part * g.rope_d) >> 6;
+    const int i = c1 & 63;
+    if (part < 2) {
+      const int pos = g.rope_pos[row];
+      const float c = g.rope_cos[pos * 32 + i], sn = g.rope_sin[pos * 32 + i];
+      const float y1 = x1 * c - x2 * sn, y2 = x1 * sn + x2 * c;
+      x1 = y1;
+      x2 = y2;
+    }
+    uint16_t* dst = part == 0 ? g.rope_q : (part == 1 ? g.rope_k : g.rope_v);
+    uint16_t* o = dst + (size_t(head) * g.rope_T + row) * 64;
+    o[i] = f2bf(x1);
+    o[i + 32] = f2bf(x2);
+    return;
+  }
+  const float b1 = g.bias ? g.bias[c1] : 0.0f, b2 = g.bias ? g.bias[c2] : 0.0f;
+  x1 += b1;
+  x2 += b2;
+  if (g.epi == EPI_RESID || g.epi == EPI_F32) {
+    float* C = reinterpret_cast<float*>(g.C) + size_t(row) * g.ldc;
+    if (g.epi == EPI_RESID) {
+      C[c1] += x1;
+      C[c2] += x2;
+    } else {
+      C[c1] = x1;
+      C[c2] = x2;
+    }
+    return;
+  }
+  if (g.act == ACT_RELU) {
+    x1 = fmaxf(x1, 0.0f);
+    x2 = fmaxf(x2, 0.0f);
+  } else if (g.act == ACT_GELU) {
+    x1 = gelu_erf(x1);
+    x2 = gelu_erf(x2);
+  }
+  uint16_t* C = reinterpret_cast<uint16_t*>(g.C) + size_t(row) * g.ldc;
+  C[c1] = f2bf(x1);
+  C[c2] = f2bf(x2);
 }
 
 }  // namespace
+
+GemmPlan gemm_plan(int M, int N, int K) {
+  GemmPlan p;
+  const int bm = M <= 64 ? 64 : 128;
+  const int tiles = ((M + bm - 1) / bm) * (N / 128);
+  const int KT = K / BK;
+  // Few tiles (small M): split K so the workgroups cover the 256 CUs about twice, each keeping
+  // at least 2 k-tiles.
+  int s = 1;
+  if (tiles < 192) s = std::max(1, std::min(KT / 2, (512 + tiles - 1) / tiles));
+  p.splits = s;
+  p.ws_floats = s > 1 ? size_t(s) * M * N : 0;
+  return p;
+}
 
 const char* gemm_check(const GemmArgs& g) {
   if (g.M <= 0) return "gemm: M must be positive";
@@ -231,10 +376,18 @@ const char* gemm_check(const GemmArgs& g) {
   if (g.N <= 0 || g.N % 128) return "gemm: N must be a positive multiple of 128";
   if (g.lda < g.K || g.ldw < g.K || (g.lda % 8) || (g.ldw % 8)) return "gemm: bad leading dimension";
   if (g.epi == EPI_ROPE && (g.rope_d % 64 || g.N != 3 * g.rope_d)) return "gemm: rope epilogue needs N = 3d, d % 64 == 0";
+  if (g.splits < 1 || g.splits > g.K / BK) return "gemm: splits must be in 1..K/64";
+  if (g.splits > 1 && !g.ws) return "gemm: split-K needs a workspace";
   return nullptr;
 }
 
 void gemm_launch(const GemmArgs& g, hipStream_t st) {
+  if (g.splits > 1) {
+    launch_e<EPI_F32>(g, st);  // partials only: the kernel returns before its epilogue
+    const long long n = (long long)g.M * (g.N / 2);
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, g);
+    return;
+  }
   switch (g.epi) {
     case EPI_BF16: launch_e<EPI_BF16>(g, st); break;
     case EPI_RESID: launch_e<EPI_RESID>(g, st); break;

@@ -19,6 +19,11 @@ struct GemmArgs {
   int lda = 0, ldw = 0, ldc = 0;
   int epi = EPI_BF16;
   int act = ACT_NONE;
+  // Split-K: `splits` workgroups share each output tile, each over a contiguous k-range, and
+  // write f32 partials [splits, M, N] to `ws`; a second kernel sums them in split order and runs
+  // the epilogue. splits = 1 runs the epilogue in the GEMM and needs no workspace.
+  int splits = 1;
+  float* ws = nullptr;
   // EPI_ROPE only
   uint16_t* rope_q = nullptr;  // [H, rope_T, 64]
   uint16_t* rope_k = nullptr;
@@ -33,6 +38,14 @@ struct GemmArgs {
 // Null when the shape is supported, else a message.
 const char* gemm_check(const GemmArgs& g);
 void gemm_launch(const GemmArgs& g, hipStream_t st);
+
+// The split-K factor gemm_launch should use for M x N x K (1: none), and the workspace it needs
+// in f32 elements.
+struct GemmPlan {
+  int splits;
+  size_t ws_floats;
+};
+GemmPlan gemm_plan(int M, int N, int K);
 
 // Attention over packed variable-length rows. q, k, v are [H, Tq or Tk, 64] bf16 (head-major).
 // Queries are numbered by output slot; each work tile is up to 128 consecutive slots of one

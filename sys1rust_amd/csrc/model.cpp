@@ -58,6 +58,7 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "unpad") s.unpad = flag();
     else if (key == "fuserope") s.fuserope = flag();
     else if (key == "fusegeglu") s.fusegeglu = flag();
+    else if (key == "graphs") s.graphs = flag();
     else if (key == "parallel_load") flag();  // read by the runtime (backend.rs:44-69); checked here too
     else if (key == "pad") {
       if (!has_val) bad("needs a value (`key=value`)");
@@ -100,6 +101,7 @@ struct Model::Acts {
   uint16_t* s1;       // [R, S]
   float* logits;      // [R]
   float* pooled;      // [n, d]
+  float* ws;          // split-K partials of the largest GEMM that splits
 };
 
 Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, const std::string& enc_json,
@@ -291,6 +293,7 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
 Model::~Model() {
   // Teardown: errors here have nowhere to go, the process keeps running.
   if (stream) (void)hipStreamSynchronize(stream);
+  drop_graphs();
   for (auto& r : pending) {
     (void)hipEventDestroy(r.a);
     (void)hipEventDestroy(r.b);
@@ -444,7 +447,11 @@ void Model::upload(const Plan& p) {
     hip_check(hipHostMalloc(&hmeta, hmeta_cap, hipHostMallocDefault), "hipHostMalloc(meta)");
   }
   if (bytes > dmeta_cap) {
-    if (dmeta) hip_check(hipFree(dmeta), "hipFree");
+    drop_graphs();
+    if (dmeta) {
+      hip_check(hipStreamSynchronize(stream), "sync");
+      hip_check(hipFree(dmeta), "hipFree");
+    }
     dmeta_cap = std::max(bytes, dmeta_cap * 3 / 2);
     hip_check(hipMalloc(&dmeta, dmeta_cap), "hipMalloc(meta)");
   }
@@ -458,9 +465,16 @@ Model::Acts Model::arena(const Plan& p) {
   const size_t T = size_t(p.T), P = size_t(p.P), R = size_t(p.R), n = size_t(p.n);
   const size_t d = size_t(cfg.d), I = size_t(cfg.inter), S = size_t(scorer_width);
   const size_t midw = std::max(2 * I, 4 * d);
+  // Split-K workspace: the largest of the forward's GEMMs that split (small M only).
+  size_t wsf = 0;
+  const int Ti = p.T, Pi = p.P, Ri = p.R, di = cfg.d, Ii = cfg.inter, Si = scorer_width;
+  const int shapes[][3] = {{Ti, 3 * di, di}, {Ti, di, di}, {Ti, 2 * Ii, di}, {Ti, di, Ii}, {Ti, 4 * di, di},
+                           {Ti, di, 4 * di}, {Pi, di, di}, {Pi, 4 * di, di}, {Pi, di, 4 * di}, {Ri, Si, di}};
+  for (const auto& sh : shapes)
+    if (sh[0] > 0) wsf = std::max(wsf, gemm_plan(sh[0], sh[1], sh[2]).ws_floats);
   size_t sizes[] = {T * d * 4, T * d * 2, T * d * 2, T * d * 2, T * d * 2, T * 3 * d * 2, T * d * 2,
                     T * midw * 2, T * I * 2, T * d * 4, T * d * 4, P * d * 4, P * d * 2, P * d * 2,
-                    P * 4 * d * 2, R * d * 2, R * S * 2, R * 4, n * d * 4};
+                    P * 4 * d * 2, R * d * 2, R * S * 2, R * 4, n * d * 4, wsf * 4};
   constexpr int NS = sizeof(sizes) / sizeof(sizes[0]);
   size_t off[NS], total = 0;
   for (int i = 0; i < NS; ++i) {
@@ -468,6 +482,7 @@ Model::Acts Model::arena(const Plan& p) {
     total += align256(std::max<size_t>(sizes[i], 16));
   }
   if (total > acap) {
+    drop_graphs();
     if (amem) {
       hip_check(hipStreamSynchronize(stream), "sync");
       hip_check(hipFree(amem), "hipFree(arena)");
@@ -498,6 +513,7 @@ Model::Acts Model::arena(const Plan& p) {
   a.s1 = reinterpret_cast<uint16_t*>(b + off[16]);
   a.logits = reinterpret_cast<float*>(b + off[17]);
   a.pooled = reinterpret_cast<float*>(b + off[18]);
+  a.ws = reinterpret_cast<float*>(b + off[19]);
   return a;
 }
 
@@ -545,9 +561,11 @@ void Model::collect_stats() {
 
 namespace {
 
-void gemm(hipStream_t st, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc, const float* bias,
-          int M, int N, int epi, int act = ACT_NONE) {
+void gemm(hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
+          const float* bias, int M, int N, int epi, int act = ACT_NONE) {
   GemmArgs g;
+  g.splits = gemm_plan(M, N, K).splits;
+  g.ws = ws;
   g.A = A;
   g.W = W;
   g.C = C;
@@ -601,11 +619,13 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
         g.rope_sin = rope_sin[tw];
         g.rope_T = T;
         g.rope_d = d;
+        g.splits = gemm_plan(T, 3 * d, d).splits;
+        g.ws = a.ws;
         if (const char* e = gemm_check(g)) fail(kBackend, e);
         gemm_launch(g, stream);
       });
     } else {
-      op("wqkv", [&] { gemm(stream, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
+      op("wqkv", [&] { gemm(stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
       op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, stream); });
     }
     op(L.local ? "attn_local" : "attn_global", [&] {
@@ -625,27 +645,85 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       attn_launch(at, stream);
     });
     // h = h + att . Wo^T (lib.rs:1666)
-    op("wo", [&] { gemm(stream, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID); });
+    op("wo", [&] { gemm(stream, a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID); });
     op("mlp_norm", [&] {
       layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
     });
     if (set.fusegeglu) {
-      op("wi_geglu", [&] { gemm(stream, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
+      op("wi_geglu", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
     } else {
-      op("wi", [&] { gemm(stream, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
+      op("wi", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
       op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream); });
     }
     // h = h + act . Wo2^T (lib.rs:1675)
-    op("wo2", [&] { gemm(stream, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID); });
+    op("wo2", [&] { gemm(stream, a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID); });
   }
 }
 
-void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
-  if (p.n == 0) return;
-  const auto t0 = std::chrono::steady_clock::now();
-  hip_check(hipSetDevice(device), "hipSetDevice");
-  upload(p);
-  Acts a = arena(p);
+// Enqueue one forward's kernels: eagerly the first time a shape is seen, then from a captured
+// HIP graph (one per shape, kept until the buffers it points into move). The graph holds
+// kernel nodes only; the batch tables are uploaded into the same device buffer before each
+// replay, and outputs are copied after it, on the same stream.
+template <class F>
+void Model::run(const Plan& p, int kind, F&& enqueue) {
+  if (!set.graphs || set.ops) {
+    enqueue();
+    hip_check(hipGetLastError(), "kernel launch");
+    return;
+  }
+  std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.ntiles, p.nptiles, p.P, p.R,
+                              int64_t(p.off_ids), int64_t(p.off_pos), int64_t(p.off_seg), int64_t(p.off_tiles),
+                              int64_t(p.off_ptiles), int64_t(p.off_picked), int64_t(p.off_scorer),
+                              int64_t(p.off_pooled), int64_t(reinterpret_cast<intptr_t>(amem)),
+                              int64_t(reinterpret_cast<intptr_t>(dmeta))};
+  ++graph_clock;
+  for (auto& g : graphs)
+    if (g.key == key) {
+      g.last_use = graph_clock;
+      hip_check(hipGraphLaunch(g.exec, stream), "hipGraphLaunch");
+      return;
+    }
+  bool seen_before = false;
+  for (const auto& k : graph_seen) seen_before = seen_before || k == key;
+  if (!seen_before) {
+    if (graph_seen.size() >= 64) graph_seen.erase(graph_seen.begin());
+    graph_seen.push_back(key);
+    enqueue();
+    hip_check(hipGetLastError(), "kernel launch");
+    return;
+  }
+  hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  hipGraph_t graph = nullptr;
+  try {
+    enqueue();
+  } catch (...) {
+    (void)hipStreamEndCapture(stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  hip_check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  hip_check(ie, "hipGraphInstantiate");
+  if (graphs.size() >= kMaxGraphs) {
+    size_t lru = 0;
+    for (size_t i = 1; i < graphs.size(); ++i)
+      if (graphs[i].last_use < graphs[lru].last_use) lru = i;
+    (void)hipGraphExecDestroy(graphs[lru].exec);
+    graphs.erase(graphs.begin() + lru);
+  }
+  graphs.push_back({key, exec, graph_clock});
+  hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+}
+
+void Model::drop_graphs() {
+  for (auto& g : graphs) (void)hipGraphExecDestroy(g.exec);
+  graphs.clear();
+  graph_seen.clear();
+}
+
+void Model::enqueue_forward(const Plan& p, const Acts& a) {
   const int T = p.T, d = cfg.d, P = p.P, R = p.R, n = p.n, S = scorer_width;
   const float eps = float(cfg.eps);
   const int* seg = dmeta + p.off_seg;
@@ -664,7 +742,7 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
     op("head_norm1", [&] {
       layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
     });
-    op("head_in_proj", [&] { gemm(stream, a.x, d, Hw.in_w, d, a.qkv, 3 * d, Hw.in_b, T, 3 * d, EPI_BF16); });
+    op("head_in_proj", [&] { gemm(stream, a.ws, a.x, d, Hw.in_w, d, a.qkv, 3 * d, Hw.in_b, T, 3 * d, EPI_BF16); });
     op("head_split", [&] { split_rope_launch(a.qkv, T, d, nullptr, nullptr, nullptr, a.q, a.k, a.v, stream); });
     if (!pruned) {
       op("head_attn", [&] {
@@ -682,12 +760,12 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
         at.scale = hscale;
         attn_launch(at, stream);
       });
-      op("head_out_proj", [&] { gemm(stream, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(stream, a.ws, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
       op("head_norm2", [&] {
         layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
       });
-      op("head_linear1", [&] { gemm(stream, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(stream, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(stream, a.ws, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(stream, a.ws, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
     } else {
       // headprune (lib.rs:1728-1748): every token supplies k and v; queries, out_proj, norm2 and
       // the FFN run at rows {0, markers} only.
@@ -709,12 +787,12 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
         attn_launch(at, stream);
       });
       op("head_pick", [&] { gather_f32_launch(a.hh, picked, P, d, a.hp, stream); });
-      op("head_out_proj", [&] { gemm(stream, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(stream, a.ws, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
       op("head_norm2", [&] {
         layernorm_launch(a.hp, nullptr, Hw.n2w, Hw.n2b, 1e-5f, P, d, a.xp, nullptr, nullptr, nullptr, nullptr, stream);
       });
-      op("head_linear1", [&] { gemm(stream, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(stream, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(stream, a.ws, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(stream, a.ws, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
     }
   }
   // score (lib.rs:1768-1800): LN_b at the marker rows, scorer1 + GELU, scorer3; pooled row 0.
@@ -725,10 +803,20 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
     op("scorer_norm", [&] {
       layernorm_launch(src, srows, sc0_w, sc0_b, 1e-5f, R, d, a.sx, nullptr, nullptr, nullptr, nullptr, stream);
     });
-    op("scorer1", [&] { gemm(stream, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
+    op("scorer1", [&] { gemm(stream, a.ws, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
     op("scorer3", [&] { rowdot_launch(a.s1, sc3_w, sc3_b, R, S, a.logits, stream); });
   }
   op("pooled", [&] { gather_f32_launch(src, prows, n, d, a.pooled, stream); });
+}
+
+void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
+  if (p.n == 0) return;
+  const auto t0 = std::chrono::steady_clock::now();
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  upload(p);
+  Acts a = arena(p);
+  const int d = cfg.d, R = p.R, n = p.n;
+  run(p, 0, [&] { enqueue_forward(p, a); });
   hip_check(hipGetLastError(), "kernel launch");
 
   const size_t out_bytes = size_t(R) * 4 + size_t(n) * d * 4;
@@ -757,12 +845,13 @@ void Model::encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden) {
   upload(p);
   Acts a = arena(p);
   const int T = p.T, d = cfg.d;
-  run_encoder(p, a);
-  op("final_norm", [&] {
-    layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, nullptr, nullptr,
-                     nullptr, stream);
+  run(p, 1, [&] {
+    run_encoder(p, a);
+    op("final_norm", [&] {
+      layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, nullptr, nullptr,
+                       nullptr, stream);
+    });
   });
-  hip_check(hipGetLastError(), "kernel launch");
   std::vector<float> packed(size_t(T) * d);
   hip_check(hipMemcpyAsync(packed.data(), a.enc, packed.size() * 4, hipMemcpyDeviceToHost, stream), "download hidden");
   hip_check(hipStreamSynchronize(stream), "encoder_hidden");

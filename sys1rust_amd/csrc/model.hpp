@@ -22,6 +22,7 @@ struct Settings {
   bool unpad = true;       // accepted; the HIP path always runs the packed token layout
   bool fuserope = true;    // RoPE + split fused into the Wqkv GEMM epilogue
   bool fusegeglu = true;   // GeGLU fused into the Wi GEMM epilogue (Wi rows interleaved at load)
+  bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
   size_t pad = 1;          // padded_len multiple
   std::vector<size_t> buckets;
   static Settings parse(const std::string& spec);
@@ -120,6 +121,17 @@ struct Model {
   std::vector<hipEvent_t> event_pool;
   std::vector<std::pair<std::string, std::pair<uint64_t, double>>> stats;
 
+  // HIP graphs of repeated batch shapes (Settings::graphs)
+  struct GraphEntry {
+    std::vector<int64_t> key;
+    hipGraphExec_t exec;
+    uint64_t last_use;
+  };
+  static constexpr size_t kMaxGraphs = 32;
+  std::vector<GraphEntry> graphs;
+  std::vector<std::vector<int64_t>> graph_seen;
+  uint64_t graph_clock = 0;
+
   Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, const std::string& enc_json,
         const std::string& agent_json, const std::string& settings, int device);
   ~Model();
@@ -136,6 +148,10 @@ struct Model {
   Acts arena(const Plan& p);
   void upload(const Plan& p);
   void run_encoder(const Plan& p, const Acts& a);
+  void enqueue_forward(const Plan& p, const Acts& a);
+  template <class F>
+  void run(const Plan& p, int kind, F&& enqueue);
+  void drop_graphs();
   template <class F>
   void op(const char* name, F&& f);
   void collect_stats();

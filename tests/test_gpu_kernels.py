@@ -89,8 +89,9 @@ def test_gemm_f32_and_bf16_outputs(dev, M, N, K):
     assert bool((err <= ref.abs() * 2 ** -8 + 1e-5 * scale).all()), float(err.max())
 
 
-def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev):
-    M, N, K = 300, 1024, 512
+@pytest.mark.parametrize("M", [300, 1500])  # split-K (reduce kernel) and whole-K epilogues
+def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M):
+    N, K = 1024, 512
     g = torch.Generator(device="cpu").manual_seed(5)
     A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
     W = bf16_bits(torch.randn(N, K, generator=g) * 0.05).to(dev)
@@ -119,12 +120,13 @@ def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev):
     assert bool(((act - r).abs() <= r.abs() * 2 ** -7 + 1e-4).all()), float((act - r).abs().max())
 
 
+@pytest.mark.parametrize("M", [512, 2048])
 @pytest.mark.parametrize("theta", [160000.0, 10000.0])
-def test_fused_wqkv_split_rope_m512(dev, theta):
-    """Isolated fused Wqkv GEMM + split + RoPE: M=512, K=1024, N=3072, A ~ N(0,1), W ~ N(0,0.02),
-    positions 0..511."""
-    say(f"qkv_rope theta={theta}")
-    M, d = 512, 1024
+def test_fused_wqkv_split_rope(dev, theta, M):
+    """Isolated fused Wqkv GEMM + split + RoPE at M=512 (and 2048, the whole-K path), K=1024,
+    N=3072, A ~ N(0,1), W ~ N(0,0.02), positions 0..M-1."""
+    say(f"qkv_rope theta={theta} M={M}")
+    d = 1024
     g = torch.Generator(device="cpu").manual_seed(int(theta) % 97)
     A = bf16_bits(torch.randn(M, d, generator=g)).to(dev)
     W = bf16_bits(torch.randn(3 * d, d, generator=g) * 0.02).to(dev)

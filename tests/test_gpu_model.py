@@ -115,6 +115,24 @@ def test_settings_variants_agree(small_model, settings):
         assert "headprune" not in var.active_kernels()
 
 
+def test_graph_replays_match_eager_runs(small_model):
+    """Repeated shapes replay a captured HIP graph: every replay, interleaved with other shapes
+    and with eager work, gives the eager path's bits."""
+    cfg, agent, st, b, z = small_model
+    say("graphs: replay vs eager")
+    g = HipBackend(st, json.dumps(cfg), json.dumps(agent))
+    e = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="graphs=0")
+    b2 = b.rows([1, 2])
+    want = {0: e.forward(b), 1: e.forward(b2)}
+    want_h = e.encoder_hidden(b)
+    for i, (k, bb) in enumerate([(0, b), (0, b), (1, b2), (0, b), (1, b2), (1, b2), (0, b), (0, b)]):
+        out = g.forward(bb)
+        assert np.array_equal(out.logits, want[k].logits), i
+        assert np.array_equal(out.pooled, want[k].pooled), i
+        if i % 3 == 0:
+            assert np.array_equal(g.encoder_hidden(b), want_h), i
+
+
 @pytest.fixture(scope="module")
 def large():
     say("large: synth checkpoint")
@@ -156,9 +174,10 @@ def test_modernbert_large_ten_questions(large):
     lg_ref, _ = o.forward(sub, ref)
     lg = out.logits.reshape(b.n, b.kmax)[rows].reshape(-1)
     check_answers(lg, lg_ref, sub, "state512_10q")
-    # rows are independent: the same rows alone give the same logits
+    # Rows are independent: the same rows alone give the same answers. (A smaller batch takes
+    # other GEMM splits, so bf16 rounding differs in the last bits; compare at the answer gates.)
     alone = m.forward(sub)
-    assert np.abs(alone.logits - lg).max() <= 1e-3
+    check_answers(alone.logits, lg, sub, "state512_10q rows alone")
 
 
 def test_warmup_and_repeat_determinism(large):
