@@ -56,6 +56,9 @@ def main() -> int:
     ap.add_argument("--settings", default="")
     ap.add_argument("--no-context", action="store_true",
                     help="time only the headline workload (no 1-question shapes), e.g. under a profiler")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run 3 plain device-to-device copies of this many MiB: the known-size "
+                         "reference that scales profiler byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -69,6 +72,14 @@ def main() -> int:
     from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, SCORER_WIDTH, workload
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_mib:
+        src = torch.empty(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1.0)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     enc_json, agent_json = json.dumps(MODERNBERT_LARGE), json.dumps(AGENT)
     t0 = time.time()
     ckpt = synth_checkpoint(enc_json, agent_json, seed=args.seed, scorer_width=SCORER_WIDTH)
