@@ -121,19 +121,21 @@ int s1k_gemm(const void* A, int lda, const void* W, int ldw, void* C, int ldc, c
              int M, int N, int K, int epi, int act, void* stream);
 
 /* Wqkv product with the q|k|v split and RoPE fused in its epilogue (the fuserope path):
- * A [M, d] bf16, W [3d, d] bf16, pos [M] int32 positions, theta the RoPE base; writes q, k, v
- * as [d/64, M, 64] bf16 each. */
+ * A [M, d] bf16, W [3d, d] bf16, pos [M] int32 positions, theta the RoPE base; writes q and k
+ * as [d/64, M, 64] bf16 and v transposed as [d/64, 64, v_ld] bf16 (v_ld a multiple of 8,
+ * at least M + 64: the layout the attention kernel reads). */
 int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos, double theta,
-                 void* q, void* k, void* v, void* stream);
+                 void* q, void* k, void* v, int v_ld, void* stream);
 
-/* Standalone split + RoPE pass: qkv [M, 3d] bf16 -> q, k, v [d/64, M, 64] bf16. theta <= 0
- * means no rotation (the decision head's split). */
+/* Standalone split + RoPE pass: qkv [M, 3d] bf16 -> q, k [d/64, M, 64] bf16 and v transposed
+ * [d/64, 64, v_ld] bf16. theta <= 0 means no rotation (the decision head's split). */
 int s1k_split_rope(const void* qkv, int M, int d, const int32_t* pos, double theta, void* q,
-                   void* k, void* v, void* stream);
+                   void* k, void* v, int v_ld, void* stream);
 
-/* Attention over packed rows: q, k, v [H, T, 64] bf16, seq_starts [nseq + 1] int32 (host
- * memory), window < 0 for global, else |i - j| <= window; out [T, H*64] bf16. */
-int s1k_attention(const void* q, const void* k, const void* v, int T, int H,
+/* Attention over packed rows: q, k [H, T, 64] bf16, v transposed [H, 64, v_ld] bf16 (v_ld >=
+ * T rounded up to 8, plus 64), seq_starts [nseq + 1] int32 (host memory), window < 0 for
+ * global, else |i - j| <= window; out [T, H*64] bf16. */
+int s1k_attention(const void* q, const void* k, const void* v, int v_ld, int T, int H,
                   const int32_t* seq_starts, int nseq, int window, float scale, void* out,
                   void* stream);
 

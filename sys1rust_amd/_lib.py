@@ -72,16 +72,17 @@ SIGNATURES = {
     "s1k_qkv_rope": (
         C.c_int,
         [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p,
-         C.c_void_p],
+         C.c_int, C.c_void_p],
     ),
     "s1k_split_rope": (
         C.c_int,
-        [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+        [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+         C.c_void_p],
     ),
     "s1k_attention": (
         C.c_int,
-        [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, i32p, C.c_int, C.c_int, C.c_float, C.c_void_p,
-         C.c_void_p],
+        [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, i32p, C.c_int, C.c_int, C.c_float,
+         C.c_void_p, C.c_void_p],
     ),
     "s1k_layernorm": (
         C.c_int,
@@ -106,6 +107,11 @@ def lib() -> C.CDLL:
             f.argtypes = args
         _lib = l
     return _lib
+
+
+def vt_ld(T: int) -> int:
+    """Row stride of a transposed v buffer for T tokens (T rounded up to 8, plus 64)."""
+    return (T + 7) // 8 * 8 + 64
 
 
 def check(rc: int) -> None:

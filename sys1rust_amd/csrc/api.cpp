@@ -315,10 +315,11 @@ int max_pos_of(const int32_t* pos, int M, hipStream_t st) {
 }  // namespace
 
 int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos, double theta, void* q, void* k, void* v,
-                 void* stream) {
+                 int v_ld, void* stream) {
   return guard([&] {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (theta <= 0) s1::fail(s1::kConfig, "s1k_qkv_rope: theta must be positive");
+    if (v_ld % 8 || v_ld < M + 64) s1::fail(s1::kConfig, "s1k_qkv_rope: v_ld must be a multiple of 8 and >= M + 64");
     rope_table(g_rope, theta, max_pos_of(pos, M, st), st);
     s1::GemmArgs g;
     g.A = static_cast<const uint16_t*>(A);
@@ -337,6 +338,7 @@ int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos,
     g.rope_sin = g_rope.s;
     g.rope_T = M;
     g.rope_d = d;
+    g.rope_ldv = v_ld;
     const s1::GemmPlan gp = s1::gemm_plan(M, 3 * d, d);
     g.splits = gp.splits;
     g.ws = workspace(gp.ws_floats, st);
@@ -347,10 +349,11 @@ int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos,
 }
 
 int s1k_split_rope(const void* qkv, int M, int d, const int32_t* pos, double theta, void* q, void* k, void* v,
-                   void* stream) {
+                   int v_ld, void* stream) {
   return guard([&] {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (d % 64) s1::fail(s1::kConfig, "s1k_split_rope: d must be a multiple of 64");
+    if (v_ld < M) s1::fail(s1::kConfig, "s1k_split_rope: v_ld must be at least M");
     const float* c = nullptr;
     const float* s = nullptr;
     if (theta > 0) {
@@ -359,24 +362,26 @@ int s1k_split_rope(const void* qkv, int M, int d, const int32_t* pos, double the
       s = g_rope.s;
     }
     s1::split_rope_launch(static_cast<const uint16_t*>(qkv), M, d, pos, c, s, static_cast<uint16_t*>(q),
-                          static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), st);
+                          static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), v_ld, st);
     hip_ok(hipGetLastError(), "s1k_split_rope launch");
   });
 }
 
-int s1k_attention(const void* q, const void* k, const void* v, int T, int H, const int32_t* seq_starts, int nseq,
-                  int window, float scale, void* out, void* stream) {
+int s1k_attention(const void* q, const void* k, const void* v, int v_ld, int T, int H, const int32_t* seq_starts,
+                  int nseq, int window, float scale, void* out, void* stream) {
   return guard([&] {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (!seq_starts || nseq < 1) s1::fail(s1::kConfig, "s1k_attention: need seq_starts");
     if (seq_starts[0] != 0 || seq_starts[nseq] != T) s1::fail(s1::kConfig, "s1k_attention: seq_starts must run 0..T");
+    if (v_ld < s1::vt_ld(T)) s1::fail(s1::kConfig, "s1k_attention: v_ld must be at least T rounded up to 8, plus 64");
+    const int qb = s1::attn_tile_queries(window >= 0);
     std::vector<int> tiles;
     for (int r = 0; r < nseq; ++r) {
       const int rs = seq_starts[r], re = seq_starts[r + 1];
       if (re <= rs) s1::fail(s1::kConfig, "s1k_attention: empty or decreasing sequence");
-      for (int q0 = rs; q0 < re; q0 += 128) {
+      for (int q0 = rs; q0 < re; q0 += qb) {
         tiles.push_back(q0);
-        tiles.push_back(std::min(q0 + 128, re));
+        tiles.push_back(std::min(q0 + qb, re));
         tiles.push_back(rs);
         tiles.push_back(re);
       }
@@ -394,6 +399,7 @@ int s1k_attention(const void* q, const void* k, const void* v, int T, int H, con
     a.heads = H;
     a.Tq = T;
     a.Tk = T;
+    a.ldv = v_ld;
     a.ldo = H * 64;
     a.scale = scale;
     a.window = window;

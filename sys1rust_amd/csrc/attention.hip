@@ -9,9 +9,11 @@
 // so a hard mask over the row's own keys computes the same values; padding never enters the
 // packed layout at all.
 //
-// Work split: a workgroup of 4 wavefronts takes up to 128 queries of one sequence and one head;
-// each wave owns 32 queries. Keys stream through LDS in chunks of 64 (K as [key][dim], V
-// transposed as [dim][key]); waves skip chunks outside their window.
+// Work split: a workgroup of NW wavefronts takes up to 32 NW queries of one sequence and one
+// head; each wave owns 32 queries. Keys stream through LDS in chunks of 64 (double-buffered on
+// global layers): K as [key][dim] and V as [dim][key], copied with 16-byte accesses from the
+// transposed v buffer. On local layers waves skip chunks, and 32-key halves, outside their
+// window, and only chunks that cross a window or row edge pay for masking.
 //
 // The products are computed transposed so that every softmax statistic lives in one lane:
 //   S^T[key, q] = K . Q^T   (A = K rows from LDS, B = the wave's Q held in registers)
@@ -28,35 +30,41 @@ namespace s1 {
 
 namespace {
 
-constexpr int KC = 64;       // keys per chunk
-constexpr int LDS_W = 72;    // padded LDS row (bf16 elements)
+constexpr int KC = 64;     // keys per chunk
+constexpr int LDS_W = 72;  // padded LDS row (bf16 elements)
 constexpr float NEG_INF = -__builtin_huge_valf();
 
-template <bool LOCAL>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[KC * LDS_W];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[64 * LDS_W];
+// Three waves per SIMD for the local kernel (register budget 168), four for the global one.
+template <bool LOCAL, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
+void attn_kernel(AttnArgs a) {
+  constexpr int NT = NW * 64;
+  constexpr int PIECES = 2 * KC * 8;  // 16-byte pieces per chunk: K [64][64] and V^T [64][64]
+  constexpr int PPT = PIECES / NT;    // pieces per thread
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KC * LDS_W];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][64 * LDS_W];
 
   const AttnTile tl = a.tiles[blockIdx.x];
   const int head = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5;       // lane half
-  const int col = lane & 31;      // query column within the wave
+  const int hl = lane >> 5;   // lane half
+  const int col = lane & 31;  // query column within the wave
 
   const uint16_t* __restrict__ Qh = a.q + size_t(head) * a.Tq * 64;
   const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.Tk * 64;
-  const uint16_t* __restrict__ Vh = a.v + size_t(head) * a.Tk * 64;
+  const uint16_t* __restrict__ Vt = a.v + size_t(head) * 64 * a.ldv;
 
   const int wq0 = tl.q0 + wave * 32;
   const bool wave_active = wq0 < tl.q1;
   const int qi = wq0 + col;
   const bool qvalid = qi < tl.q1;
   const int qld = min(qi, tl.q1 - 1);
-  const int qk = a.qkey ? a.qkey[qld] : qld;  // key-buffer index of this query
+  const int qk = a.qkey ? a.qkey[qld] : qld;  // q row and key index of this query
 
   // Key range of the workgroup and of this wave.
   int kb0 = tl.k0, kb1 = tl.k1;
   int wk0 = tl.k0, wk1 = tl.k1;
+  int wf_key = 0, wl_key = 0;  // key index of the wave's first and last query (local layers)
   if constexpr (LOCAL) {
     const int first = a.qkey ? a.qkey[tl.q0] : tl.q0;
     const int last = a.qkey ? a.qkey[tl.q1 - 1] : tl.q1 - 1;
@@ -68,8 +76,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       const int wl = a.qkey ? a.qkey[wlq] : wlq;
       wk0 = max(tl.k0, wf - a.window);
       wk1 = min(tl.k1, wl + a.window + 1);
+      wf_key = wf;
+      wl_key = wl;
     }
   }
+  // Chunks start 8-aligned so the V^T rows are read with aligned 16-byte loads; keys before kb0
+  // and from kb1 on are masked (and their V entries zeroed in LDS).
+  const int cstart = kb0 & ~7;
 
   // This lane's slice of its query: dims 16kb + 8h .. +7 for kb = 0..3 (MFMA B operand).
   bf16x8 qf[4];
@@ -77,100 +90,156 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   for (int kb = 0; kb < 4; ++kb)
     qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
 
+  uint4 stage[PPT];
+  auto gload = [&](int c0) {
+#pragma unroll
+    for (int it = 0; it < PPT; ++it) {
+      const int p = tid + it * NT;
+      if (p < KC * 8) {  // K piece: key p / 8, dims (p % 8) * 8
+        const int key = p >> 3, dc = (p & 7) * 8;
+        const int kg = min(c0 + key, kb1 - 1);
+        stage[it] = *reinterpret_cast<const uint4*>(Kh + size_t(kg) * 64 + dc);
+      } else {  // V^T piece: dim q / 8, keys (q % 8) * 8
+        const int q = p - KC * 8;
+        const int dim = q >> 3, kc = (q & 7) * 8;
+        uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c0 + kc);
+        const int valid = kb1 - (c0 + kc);  // keys of this piece inside the range
+        if (valid < 8) {
+          uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          v = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        stage[it] = v;
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int it = 0; it < PPT; ++it) {
+      const int p = tid + it * NT;
+      if (p < KC * 8) {
+        *reinterpret_cast<uint4*>(&sK[buf][(p >> 3) * LDS_W + (p & 7) * 8]) = stage[it];
+      } else {
+        const int q = p - KC * 8;
+        *reinterpret_cast<uint4*>(&sVt[buf][(q >> 3) * LDS_W + (q & 7) * 8]) = stage[it];
+      }
+    }
+  };
+
   const float sl2 = a.scale * 1.4426950408889634f;  // fold log2(e): exp(x) = exp2(x log2 e)
   float m = NEG_INF, l = 0.0f;
   f32x16 o[2];
 #pragma unroll
   for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
 
-  for (int c0 = kb0; c0 < kb1; c0 += KC) {
+  // Global layers double-buffer the chunks (the next chunk's loads overlap this one's math);
+  // local layers visit few chunks per wave and keep the lighter single buffer, which leaves
+  // registers for three waves per SIMD.
+  constexpr bool DB = !LOCAL;
+  if constexpr (DB) {
+    gload(cstart);
+    sstore(0);
     __syncthreads();
-    // Stage 64 keys x 64 dims of K and V (clamped at the range end; those slots are masked).
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int c = tid + it * 256;
-      const int key = c >> 3, dc = (c & 7) * 8;
-      const int kg = min(c0 + key, kb1 - 1);
-      const uint4 kv = *reinterpret_cast<const uint4*>(Kh + size_t(kg) * 64 + dc);
-      *reinterpret_cast<uint4*>(&sK[key * LDS_W + dc]) = kv;
-      const uint4 vv = *reinterpret_cast<const uint4*>(Vh + size_t(kg) * 64 + dc);
-      sVt[(dc + 0) * LDS_W + key] = uint16_t(vv.x);
-      sVt[(dc + 1) * LDS_W + key] = uint16_t(vv.x >> 16);
-      sVt[(dc + 2) * LDS_W + key] = uint16_t(vv.y);
-      sVt[(dc + 3) * LDS_W + key] = uint16_t(vv.y >> 16);
-      sVt[(dc + 4) * LDS_W + key] = uint16_t(vv.z);
-      sVt[(dc + 5) * LDS_W + key] = uint16_t(vv.z >> 16);
-      sVt[(dc + 6) * LDS_W + key] = uint16_t(vv.w);
-      sVt[(dc + 7) * LDS_W + key] = uint16_t(vv.w >> 16);
+  }
+  int buf = 0;
+  for (int c0 = cstart; c0 < kb1; c0 += KC, buf ^= (DB ? 1 : 0)) {
+    const bool more = DB && c0 + KC < kb1;
+    if constexpr (DB) {
+      if (more) gload(c0 + KC);
+    } else {
+      if (c0 != cstart) __syncthreads();  // every wave is done with the previous chunk
+      gload(c0);
+      sstore(0);
+      __syncthreads();
     }
-    __syncthreads();
-    if (!wave_active) continue;
-    if constexpr (LOCAL) {
-      if (c0 + KC <= wk0 || c0 >= wk1) continue;
-    }
-
-    // S^T for two 32-key tiles.
-    f32x16 s[2];
+    bool work = wave_active;
+    if constexpr (LOCAL) work = work && !(c0 + KC <= wk0 || c0 >= wk1);
+    if (work) {
+      // 32-key tiles of this chunk that hold keys this wave may see (local layers skip the rest).
+      bool need[2] = {true, true};
+      if constexpr (LOCAL) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[t][e] = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[(t * 32 + col) * LDS_W + kb * 16 + hl * 8]);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+        for (int t = 0; t < 2; ++t) need[t] = c0 + 32 * t < wk1 && c0 + 32 * t + 32 > wk0;
       }
-    }
-    // Scale (base-2 logits) and mask.
-    float mx = NEG_INF;
+      // Masks are needed only where the chunk crosses the key range or some query's window.
+      bool edge = c0 < kb0 || c0 + KC > kb1;
+      if constexpr (LOCAL) edge = edge || c0 < wl_key - a.window || c0 + KC > wf_key + a.window + 1;
+      // S^T for the needed 32-key tiles (raw logits; masked entries -inf).
+      f32x16 s[2];
+      float mx = NEG_INF;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = c0 + t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
-        bool ok = key < kb1;
-        if constexpr (LOCAL) ok = ok && abs(key - qk) <= a.window;
-        const float v = ok ? s[t][e] * sl2 : NEG_INF;
-        s[t][e] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx);
-    const float alpha = (m == NEG_INF) ? 0.0f : exp2f(m - mn);
-    float psum = 0.0f;
-    bf16x8 pf[2][2];
+        for (int e = 0; e < 16; ++e) s[t][e] = 0.0f;
+        if (!need[t]) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = s[t][sb * 8 + j];
-          const float p = (v == NEG_INF) ? 0.0f : exp2f(v - mn);
-          psum += p;
-          pf[t][sb][j] = __bf16(p);
+          for (int e = 0; e < 16; ++e) s[t][e] = NEG_INF;
+          continue;
         }
-    l = l * alpha + psum;
-    m = mn;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+        for (int kb = 0; kb < 4; ++kb) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][(t * 32 + col) * LDS_W + kb * 16 + hl * 8]);
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+        }
+        if (edge) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = c0 + t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+            bool ok = key >= kb0 && key < kb1;
+            if constexpr (LOCAL) ok = ok && abs(key - qk) <= a.window;
+            s[t][e] = ok ? s[t][e] : NEG_INF;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+      }
+      // Online softmax in base 2: p = 2^(s * sl2 - m). sl2 > 0, so the raw max scales.
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m, mx * sl2);
+      const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is exp2(-inf) = 0
+      const float alpha = exp2f(m - ms);
+      float psum = 0.0f;
+      bf16x8 pf[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float p = exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
+            psum += p;
+            pf[t][sb][j] = __bf16(p);
+          }
+      l = l * alpha + psum;
+      m = mn;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
 
-    // O^T += V^T . P^T over the 64 keys (4 MFMA k-steps of 16 keys) for both 32-dim halves.
+      // O^T += V^T . P^T over the needed tiles (MFMA k-steps of 16 keys), both 32-dim halves.
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
+        if (!need[t]) continue;
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        const int kbase = t * 32 + sb * 16 + hl * 4;
+        for (int sb = 0; sb < 2; ++sb) {
+          const int kbase = t * 32 + sb * 16 + hl * 4;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const uint16_t* vr = &sVt[(dt * 32 + col) * LDS_W];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
-          const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+          for (int dt = 0; dt < 2; ++dt) {
+            const uint16_t* vr = &sVt[buf][(dt * 32 + col) * LDS_W];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
+            const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+          }
         }
       }
+    }
+    if constexpr (DB) {
+      if (more) sstore(buf ^ 1);  // the other buffer was last read before the previous barrier
+      __syncthreads();
+    }
   }
 
   if (!wave_active) return;
@@ -192,13 +261,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 }  // namespace
 
+int attn_tile_queries(bool local) { return local ? 128 : 256; }
+
 void attn_launch(const AttnArgs& a, hipStream_t st) {
   if (a.ntiles <= 0) return;
   dim3 grid(a.ntiles, a.heads);
   if (a.window >= 0)
-    hipLaunchKernelGGL(attn_kernel<true>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<true, 4>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(attn_kernel<false>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<false, 8>), grid, dim3(512), 0, st, a);
 }
 
 }  // namespace s1

@@ -109,7 +109,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restrict__ qkv, int T, int d,
                                                         const int* __restrict__ pos, const float* __restrict__ ct,
                                                         const float* __restrict__ stab, uint16_t* __restrict__ q,
-                                                        uint16_t* __restrict__ k, uint16_t* __restrict__ v) {
+                                                        uint16_t* __restrict__ k, uint16_t* __restrict__ v,
+                                                        int ldv) {
   const int H = d >> 6;
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long long)T * H * 4) return;
@@ -151,9 +152,19 @@ __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restr
     *reinterpret_cast<uint4*>(dp) = pack8(y1);
     *reinterpret_cast<uint4*>(dp + 32) = pack8(y2);
   }
+  // v, transposed: dims i0 .. i0 + 7 and i0 + 32 .. i0 + 39 of token t.
   const uint16_t* sv = src + 2 * d;
-  *reinterpret_cast<uint4*>(v + dst) = *reinterpret_cast<const uint4*>(sv);
-  *reinterpret_cast<uint4*>(v + dst + 32) = *reinterpret_cast<const uint4*>(sv + 32);
+  const uint4 va = *reinterpret_cast<const uint4*>(sv);
+  const uint4 vb = *reinterpret_cast<const uint4*>(sv + 32);
+  uint16_t* vt = v + (size_t(head) * 64 + i0) * ldv + t;
+  const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    vt[size_t(2 * j) * ldv] = uint16_t(wa[j]);
+    vt[size_t(2 * j + 1) * ldv] = uint16_t(wa[j] >> 16);
+    vt[size_t(32 + 2 * j) * ldv] = uint16_t(wb[j]);
+    vt[size_t(33 + 2 * j) * ldv] = uint16_t(wb[j] >> 16);
+  }
 }
 
 __global__ __launch_bounds__(256) void geglu_kernel(const uint16_t* __restrict__ wi, int T, int I,
@@ -228,11 +239,11 @@ void layernorm_launch(const float* x, const int* rows, const float* w, const flo
 }
 
 void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
-                       uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t st) {
+                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st) {
   const long long n = (long long)T * (d / 64) * 4;
   if (n <= 0) return;
   hipLaunchKernelGGL(split_rope_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, T, d, pos, cos_t, sin_t,
-                     q, k, v);
+                     q, k, v, ldv);
 }
 
 void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st) {

@@ -20,8 +20,9 @@
 //   EPI_RESID  C f32 += acc (+ bias)            residual add of Wo / Wo2 / out_proj / linear2
 //   EPI_GEGLU  W rows interleaved by 32 (x block, gate block): C bf16 [M, N/2] = gelu(x) * gate
 //   EPI_F32    C f32 = acc (+ bias)
-//   EPI_ROPE   the encoder's Wqkv: split into q|k|v, RoPE on q and k (cos/sin table by token
-//              position), written head-major as [H, T, 64] bf16 each
+//   EPI_ROPE   a q|k|v product (+ bias): split, RoPE on q and k when a cos/sin table is given
+//              (by token position), q and k written head-major [H, T, 64], v transposed
+//              [H, 64, ldv], bf16; the encoder's Wqkv and the decision head's in_proj
 #include <algorithm>
 
 #include "device.hpp"
@@ -215,28 +216,57 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     // Columns [0, d) are q, [d, 2d) k, [2d, 3d) v; within a head of 64, dims i and i + 32 form a
     // rotation pair. With TN a multiple of 64 and fragments of 32 columns, fragment 2p holds dim
     // i = lane & 31 of a head and fragment 2p + 1 holds dim i + 32 of the same head, same rows.
+    // q and k go out as [H, T, 64]; v goes out transposed, [H, 64, ldv], which is the layout the
+    // attention kernel stages: a lane's 4 consecutive rows of one dim are one 8-byte store.
     const int d = g.rope_d;
+    const int i = lane & 31;
 #pragma unroll
     for (int p = 0; p < FN / 2; ++p) {
       const int c0 = n0 + wn * TN + p * 64;  // first column of this head
       const int part = c0 / d;                 // 0 q, 1 k, 2 v
       const int head = (c0 - part * d) >> 6;
-      const int i = lane & 31;
-      uint16_t* dst = part == 0 ? g.rope_q : (part == 1 ? g.rope_k : g.rope_v);
+      if (part == 2) {
+        uint16_t* v1 = g.rope_v + (size_t(head) * 64 + i) * g.rope_ldv;
+        uint16_t* v2 = v1 + size_t(32) * g.rope_ldv;
+        const float b1 = g.bias ? g.bias[c0 + i] : 0.0f, b2 = g.bias ? g.bias[c0 + 32 + i] : 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int row = rowbase + mi * 32 + q4 * 8;  // 4 rows row .. row + 3
+            const f32x16& a1 = acc[mi][2 * p];
+            const f32x16& a2 = acc[mi][2 * p + 1];
+            if (row + 3 < g.M) {
+              *reinterpret_cast<uint2*>(v1 + row) = make_uint2(pack2(a1[q4 * 4 + 0] + b1, a1[q4 * 4 + 1] + b1),
+                                                               pack2(a1[q4 * 4 + 2] + b1, a1[q4 * 4 + 3] + b1));
+              *reinterpret_cast<uint2*>(v2 + row) = make_uint2(pack2(a2[q4 * 4 + 0] + b2, a2[q4 * 4 + 1] + b2),
+                                                               pack2(a2[q4 * 4 + 2] + b2, a2[q4 * 4 + 3] + b2));
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (row + r < g.M) {
+                  v1[row + r] = f2bf(a1[q4 * 4 + r] + b1);
+                  v2[row + r] = f2bf(a2[q4 * 4 + r] + b2);
+                }
+            }
+          }
+        continue;
+      }
+      uint16_t* dst = part == 0 ? g.rope_q : g.rope_k;
+      const float b1 = g.bias ? g.bias[c0 + i] : 0.0f, b2 = g.bias ? g.bias[c0 + 32 + i] : 0.0f;
 #pragma unroll
       for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = rowbase + mi * 32 + (e >> 2) * 8 + (e & 3);
           if (row < g.M) {
-            float x1 = acc[mi][2 * p][e], x2 = acc[mi][2 * p + 1][e];
-            if (part < 2) {
+            float x1 = acc[mi][2 * p][e] + b1, x2 = acc[mi][2 * p + 1][e] + b2;
+            if (g.rope_cos) {
               const int pos = g.rope_pos[row];
               const float c = g.rope_cos[pos * 32 + i], s = g.rope_sin[pos * 32 + i];
               const float y1 = x1 * c - x2 * s;
-              const float y2 = x1 * s + x2 * c;
+              x2 = x1 * s + x2 * c;
               x1 = y1;
-              x2 = y2;
             }
             uint16_t* o = dst + (size_t(head) * g.rope_T + row) * 64;
             o[i] = f2bf(x1);
@@ -315,15 +345,24 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
     const int part = c1 / g.rope_d;
     const int head = (c1 - part * g.rope_d) >> 6;
     const int i = c1 & 63;
-    if (part < 2) {
+    if (g.bias) {
+      x1 += g.bias[c1];
+      x2 += g.bias[c2];
+    }
+    if (part < 2 && g.rope_cos) {
       const int pos = g.rope_pos[row];
       const float c = g.rope_cos[pos * 32 + i], sn = g.rope_sin[pos * 32 + i];
       const float y1 = x1 * c - x2 * sn, y2 = x1 * sn + x2 * c;
       x1 = y1;
       x2 = y2;
     }
-    uint16_t* dst = part == 0 ? g.rope_q : (part == 1 ? g.rope_k : g.rope_v);
-    uint16_t* o = dst + (size_t(head) * g.rope_T + row) * 64;
+    if (part == 2) {  // v transposed, [H, 64, ldv]
+      uint16_t* o = g.rope_v + (size_t(head) * 64 + i) * g.rope_ldv + row;
+      o[0] = f2bf(x1);
+      o[size_t(32) * g.rope_ldv] = f2bf(x2);
+      return;
+    }
+    uint16_t* o = (part == 0 ? g.rope_q : g.rope_k) + (size_t(head) * g.rope_T + row) * 64;
     o[i] = f2bf(x1);
     o[i + 32] = f2bf(x2);
     return;
@@ -376,6 +415,7 @@ const char* gemm_check(const GemmArgs& g) {
   if (g.N <= 0 || g.N % 128) return "gemm: N must be a positive multiple of 128";
   if (g.lda < g.K || g.ldw < g.K || (g.lda % 8) || (g.ldw % 8)) return "gemm: bad leading dimension";
   if (g.epi == EPI_ROPE && (g.rope_d % 64 || g.N != 3 * g.rope_d)) return "gemm: rope epilogue needs N = 3d, d % 64 == 0";
+  if (g.epi == EPI_ROPE && (g.rope_ldv % 8 || g.rope_ldv < g.M + 64)) return "gemm: v row stride must be a multiple of 8 and >= M + 64";
   if (g.splits < 1 || g.splits > g.K / BK) return "gemm: splits must be in 1..K/64";
   if (g.splits > 1 && !g.ws) return "gemm: split-K needs a workspace";
   return nullptr;

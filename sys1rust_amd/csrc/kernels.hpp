@@ -27,7 +27,8 @@ struct GemmArgs {
   // EPI_ROPE only
   uint16_t* rope_q = nullptr;  // [H, rope_T, 64]
   uint16_t* rope_k = nullptr;
-  uint16_t* rope_v = nullptr;
+  uint16_t* rope_v = nullptr;  // transposed: [H, 64, rope_ldv]
+  int rope_ldv = 0;
   const int* rope_pos = nullptr;   // [M] position of each row in its sequence
   const float* rope_cos = nullptr;  // [max_pos, 32]
   const float* rope_sin = nullptr;
@@ -47,7 +48,12 @@ struct GemmPlan {
 };
 GemmPlan gemm_plan(int M, int N, int K);
 
-// Attention over packed variable-length rows. q, k, v are [H, Tq or Tk, 64] bf16 (head-major).
+// The row stride of a transposed v buffer for T tokens: T rounded up to 8 (16-byte rows) plus
+// 64 columns of slack, so a 64-key chunk read never leaves the row.
+inline int vt_ld(int T) { return (T + 7) / 8 * 8 + 64; }
+
+// Attention over packed variable-length rows. q, k are [H, Tq or Tk, 64] bf16 (head-major) and v
+// is transposed, [H, 64, ldv] (vt_ld(Tk)).
 // Queries are numbered by output slot; each work tile is up to 128 consecutive slots of one
 // sequence: {q0, q1, k0, k1} = slots [q0, q1) and the sequence's key range [k0, k1). Slot s reads
 // q row qkey[s] (or s when qkey is null), writes out row s, and sits at key index qkey[s] for
@@ -65,12 +71,15 @@ struct AttnArgs {
   const int* qkey = nullptr;  // [slots] q row / key index of each slot, or null for identity
   int ntiles = 0;
   int heads = 0;
-  int Tq = 0, Tk = 0;  // rows of the q buffer and of the k/v buffers (head strides)
+  int Tq = 0, Tk = 0;  // rows of the q buffer and of the k buffer (head strides)
+  int ldv = 0;         // row stride of the transposed v
   int ldo = 0;
   float scale = 0.125f;
   int window = -1;  // < 0: global attention; else keys with |i - j| <= window
 };
 void attn_launch(const AttnArgs& a, hipStream_t st);
+// Queries per work tile the attention kernel takes (global layers use larger workgroups).
+int attn_tile_queries(bool local);
 
 // h[t] = LN(tok_emb[ids[t]]) (no bias), written as f32 and as bf16.
 void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
@@ -83,9 +92,10 @@ void layernorm_launch(const float* x, const int* rows, const float* w, const flo
                       uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
                       hipStream_t st);
 
-// Plain split (+ RoPE when cos/sin are given): qkv [T, 3d] bf16 -> q, k, v [H, T, 64] bf16.
+// Plain split (+ RoPE when cos/sin are given): qkv [T, 3d] bf16 -> q, k [H, T, 64] and v
+// transposed [H, 64, ldv] (ldv >= T), bf16.
 void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
-                       uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t st);
+                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st);
 
 // act[t, i] = gelu(wi[t, i]) * wi[t, I + i] for the un-interleaved Wi product.
 void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st);

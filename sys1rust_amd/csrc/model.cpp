@@ -398,17 +398,24 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
     while (m.size() % 4) m.push_back(0);
   };
   pad4();
-  p.off_tiles = m.size();
-  for (uint32_t r = 0; r < n; ++r) {
-    const int rs = p.row_start[r], re = p.row_start[r + 1];
-    for (int q0 = rs; q0 < re; q0 += 128) {
-      m.push_back(q0);
-      m.push_back(std::min(q0 + 128, re));
-      m.push_back(rs);
-      m.push_back(re);
-      ++p.ntiles;
+  // Attention work tiles: query blocks of one row, 256 queries for global layers (one
+  // workgroup of 8 waves), 128 for local ones (4 waves; their keys are only the window).
+  auto tiles = [&](int qb, int& count) {
+    for (uint32_t r = 0; r < n; ++r) {
+      const int rs = p.row_start[r], re = p.row_start[r + 1];
+      for (int q0 = rs; q0 < re; q0 += qb) {
+        m.push_back(q0);
+        m.push_back(std::min(q0 + qb, re));
+        m.push_back(rs);
+        m.push_back(re);
+        ++count;
+      }
     }
-  }
+  };
+  p.off_tiles = m.size();
+  tiles(attn_tile_queries(false), p.ntiles);
+  p.off_ltiles = m.size();
+  tiles(attn_tile_queries(true), p.nltiles);
   const int per = 1 + int(kmax);
   if (set.headprune) {
     p.off_ptiles = m.size();
@@ -472,7 +479,8 @@ Model::Acts Model::arena(const Plan& p) {
                            {Ti, di, 4 * di}, {Pi, di, di}, {Pi, 4 * di, di}, {Pi, di, 4 * di}, {Ri, Si, di}};
   for (const auto& sh : shapes)
     if (sh[0] > 0) wsf = std::max(wsf, gemm_plan(sh[0], sh[1], sh[2]).ws_floats);
-  size_t sizes[] = {T * d * 4, T * d * 2, T * d * 2, T * d * 2, T * d * 2, T * 3 * d * 2, T * d * 2,
+  const size_t vbytes = d * size_t(vt_ld(int(T))) * 2;  // v transposed, [H, 64, ldv]
+  size_t sizes[] = {T * d * 4, T * d * 2, T * d * 2, T * d * 2, vbytes, T * 3 * d * 2, T * d * 2,
                     T * midw * 2, T * I * 2, T * d * 4, T * d * 4, P * d * 4, P * d * 2, P * d * 2,
                     P * 4 * d * 2, R * d * 2, R * S * 2, R * 4, n * d * 4, wsf * 4};
   constexpr int NS = sizeof(sizes) / sizeof(sizes[0]);
@@ -590,6 +598,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
   const int* ids = dmeta + p.off_ids;
   const int* pos = dmeta + p.off_pos;
   const AttnTile* tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_tiles);
+  const AttnTile* ltiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_ltiles);
 
   // h = LN(tok_emb[ids]) (lib.rs:1534-1551); x = h for layer 0, which has no attn_norm.
   op("embed_ln", [&] { embed_ln_launch(tok_emb, ids, emb_norm, eps, T, d, a.h, a.x, stream); });
@@ -619,6 +628,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
         g.rope_sin = rope_sin[tw];
         g.rope_T = T;
         g.rope_d = d;
+        g.rope_ldv = vt_ld(T);
         g.splits = gemm_plan(T, 3 * d, d).splits;
         g.ws = a.ws;
         if (const char* e = gemm_check(g)) fail(kBackend, e);
@@ -626,7 +636,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       });
     } else {
       op("wqkv", [&] { gemm(stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
-      op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, stream); });
+      op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, vt_ld(T), stream); });
     }
     op(L.local ? "attn_local" : "attn_global", [&] {
       AttnArgs at;
@@ -634,11 +644,12 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       at.k = a.k;
       at.v = a.v;
       at.out = a.att;
-      at.tiles = tiles;
-      at.ntiles = p.ntiles;
+      at.tiles = L.local ? ltiles : tiles;
+      at.ntiles = L.local ? p.nltiles : p.ntiles;
       at.heads = H;
       at.Tq = T;
       at.Tk = T;
+      at.ldv = vt_ld(T);
       at.ldo = d;
       at.scale = 1.0f / std::sqrt(float(cfg.head_dim()));
       at.window = L.local ? cfg.window() : -1;
@@ -671,7 +682,7 @@ void Model::run(const Plan& p, int kind, F&& enqueue) {
     hip_check(hipGetLastError(), "kernel launch");
     return;
   }
-  std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.ntiles, p.nptiles, p.P, p.R,
+  std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.ntiles, p.nltiles, p.nptiles, p.P, p.R, int64_t(p.off_ltiles),
                               int64_t(p.off_ids), int64_t(p.off_pos), int64_t(p.off_seg), int64_t(p.off_tiles),
                               int64_t(p.off_ptiles), int64_t(p.off_picked), int64_t(p.off_scorer),
                               int64_t(p.off_pooled), int64_t(reinterpret_cast<intptr_t>(amem)),
@@ -742,8 +753,29 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
     op("head_norm1", [&] {
       layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
     });
-    op("head_in_proj", [&] { gemm(stream, a.ws, a.x, d, Hw.in_w, d, a.qkv, 3 * d, Hw.in_b, T, 3 * d, EPI_BF16); });
-    op("head_split", [&] { split_rope_launch(a.qkv, T, d, nullptr, nullptr, nullptr, a.q, a.k, a.v, stream); });
+    // in_proj + bias with the head split fused in its epilogue (no rotation in the head)
+    op("head_in_proj", [&] {
+      GemmArgs g;
+      g.A = a.x;
+      g.W = Hw.in_w;
+      g.bias = Hw.in_b;
+      g.M = T;
+      g.N = 3 * d;
+      g.K = d;
+      g.lda = d;
+      g.ldw = d;
+      g.epi = EPI_ROPE;
+      g.rope_q = a.q;
+      g.rope_k = a.k;
+      g.rope_v = a.v;
+      g.rope_T = T;
+      g.rope_d = d;
+      g.rope_ldv = vt_ld(T);
+      g.splits = gemm_plan(T, 3 * d, d).splits;
+      g.ws = a.ws;
+      if (const char* e = gemm_check(g)) fail(kBackend, e);
+      gemm_launch(g, stream);
+    });
     if (!pruned) {
       op("head_attn", [&] {
         AttnArgs at;
@@ -756,6 +788,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.heads = cfg.head_nheads();
         at.Tq = T;
         at.Tk = T;
+        at.ldv = vt_ld(T);
         at.ldo = d;
         at.scale = hscale;
         attn_launch(at, stream);
@@ -782,6 +815,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.heads = cfg.head_nheads();
         at.Tq = T;
         at.Tk = T;
+        at.ldv = vt_ld(T);
         at.ldo = d;
         at.scale = hscale;
         attn_launch(at, stream);

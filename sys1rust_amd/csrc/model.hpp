@@ -72,9 +72,9 @@ struct Plan {
   std::vector<int> row_start;  // [n + 1]
   // device-bound tables (int32), concatenated in `meta`
   std::vector<int> meta;
-  size_t off_ids = 0, off_pos = 0, off_seg = 0, off_tiles = 0, off_ptiles = 0, off_picked = 0, off_scorer = 0,
-         off_pooled = 0, off_pseg = 0;
-  int ntiles = 0, nptiles = 0;
+  size_t off_ids = 0, off_pos = 0, off_seg = 0, off_tiles = 0, off_ltiles = 0, off_ptiles = 0, off_picked = 0,
+         off_scorer = 0, off_pooled = 0;
+  int ntiles = 0, nltiles = 0, nptiles = 0;
 };
 
 struct Model {

@@ -66,7 +66,7 @@ def gemm(A, W, M, N, K, epi=0, act=0, bias=None, C_out=None):
 
 
 def as_f32(bits):
-    return bits.view(torch.bfloat16).float()
+    return bits.contiguous().view(torch.bfloat16).float()
 
 
 SHAPES = [(1, 128, 64), (37, 256, 128), (170, 3072, 1024), (257, 1024, 1024), (563, 1024, 2624), (600, 5248, 1024),
@@ -131,10 +131,13 @@ def test_fused_wqkv_split_rope(dev, theta, M):
     A = bf16_bits(torch.randn(M, d, generator=g)).to(dev)
     W = bf16_bits(torch.randn(3 * d, d, generator=g) * 0.02).to(dev)
     pos = torch.arange(M, dtype=torch.int32, device=dev)
-    q, k, v = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(3))
     L = _lib()
-    L.check(L.lib().s1k_qkv_rope(ptr(A), ptr(W), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(v), stream()))
+    ldv = L.vt_ld(M)
+    q, k = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(2))
+    vt = torch.zeros(16, 64, ldv, dtype=torch.int16, device=dev)
+    L.check(L.lib().s1k_qkv_rope(ptr(A), ptr(W), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(vt), ldv, stream()))
     torch.cuda.synchronize()
+    v = vt[:, :, :M].transpose(1, 2)  # v is written transposed, [H, 64, ldv]
     qkv = (as_f32(A) @ as_f32(W).T).cpu().numpy()
     cos, sin = O.rope_tables(theta, M, 64)
     want = []
@@ -154,10 +157,13 @@ def test_split_rope_pass(dev, theta):
     g = torch.Generator(device="cpu").manual_seed(3)
     qkv = bf16_bits(torch.randn(M, 3 * d, generator=g)).to(dev)
     pos = torch.arange(M, dtype=torch.int32, device=dev) * 11  # positions up to 7689
-    q, k, v = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(3))
     L = _lib()
-    L.check(L.lib().s1k_split_rope(ptr(qkv), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(v), stream()))
+    ldv = L.vt_ld(M)
+    q, k = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(2))
+    vt = torch.zeros(16, 64, ldv, dtype=torch.int16, device=dev)
+    L.check(L.lib().s1k_split_rope(ptr(qkv), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(vt), ldv, stream()))
     torch.cuda.synchronize()
+    v = vt[:, :, :M].transpose(1, 2)
     x = as_f32(qkv).cpu().numpy()
     p = pos.cpu().numpy()
     for part, got in enumerate((q, k, v)):
@@ -190,7 +196,7 @@ def attention_ref(q, k, v, starts, window, scale):
 
 
 @pytest.mark.parametrize("window", [-1, 64])
-@pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048]])
+@pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048], [5, 3, 250, 1, 700, 9]])
 def test_attention_varlen(dev, window, lens):
     say(f"attention window={window} lens={lens}")
     H = 16
@@ -199,11 +205,15 @@ def test_attention_varlen(dev, window, lens):
     g = torch.Generator(device="cpu").manual_seed(T + window)
     q, k, v = (torch.randn(H, T, 64, generator=g) for _ in range(3))
     qb, kb, vb = (bf16_bits(x).to(dev) for x in (q, k, v))
-    out = torch.zeros(T, H * 64, dtype=torch.int16, device=dev)
     L = _lib()
+    ldv = L.vt_ld(T)
+    # v transposed, [H, 64, ldv]; the slack past T holds NaN bits, which must never reach the output
+    vt = torch.full((H, 64, ldv), -1, dtype=torch.int16, device=dev)
+    vt[:, :, :T] = vb.transpose(1, 2)
+    out = torch.zeros(T, H * 64, dtype=torch.int16, device=dev)
     st = np.ascontiguousarray(starts)
-    L.check(L.lib().s1k_attention(ptr(qb), ptr(kb), ptr(vb), T, H, st.ctypes.data_as(L.i32p), len(lens), window,
-                                  0.125, ptr(out), stream()))
+    L.check(L.lib().s1k_attention(ptr(qb), ptr(kb), ptr(vt), ldv, T, H, st.ctypes.data_as(L.i32p), len(lens),
+                                  window, 0.125, ptr(out), stream()))
     torch.cuda.synchronize()
     ref = attention_ref(as_f32(qb.cpu()), as_f32(kb.cpu()), as_f32(vb.cpu()), starts.tolist(), window, 0.125)
     got = as_f32(out.cpu())
