@@ -14,15 +14,18 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // bf16 values travel as raw uint16_t in memory.
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 
-// f32 -> bf16, round to nearest even (NaN stays NaN).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return uint32_t(f2bf(a)) | (uint32_t(f2bf(b)) << 16); }
+// f32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+
+// Two f32 -> two bf16 in one register (low half = a), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  bf16x2 r;
+  r[0] = static_cast<__bf16>(a);
+  r[1] = static_cast<__bf16>(b);
+  return __builtin_bit_cast(uint32_t, r);
+}
 
 // Unpack 8 bf16 held in a uint4 to floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {

@@ -5,15 +5,16 @@
 // are K-contiguous ("NT"), the layout the MFMA operands want: every lane reads 8 consecutive k
 // of one row with a single 16-byte LDS read.
 //
-// Tiling: a BM x BN x 64 block tile in 4 or 8 wavefronts; each wave owns a (BM/WM) x (BN/WN)
-// sub-tile computed with v_mfma_f32_32x32x16_bf16. Global -> register -> LDS staging is double
-// buffered so the next k-tile's loads are in flight while the current one feeds the MFMAs, with
-// one barrier per k-tile. LDS rows are padded by 16 bytes so the 16-byte operand reads of 8
-// consecutive lanes hit distinct banks.
+// Tiling: a BM x BN x 64 block tile in 4 wavefronts; each wave owns a (BM/WM) x (BN/WN) sub-tile
+// computed with v_mfma_f32_32x32x16_bf16. Operands move global -> LDS directly
+// (global_load_lds_dwordx4, no registers), STAGES k-tiles deep, one barrier per k-tile; a
+// 16-byte-chunk XOR swizzle keeps the fragment reads free of bank conflicts.
 //
-// MFMA 32x32x16 lane layout (per operand, lane l, h = l / 32): A supplies row l % 32, k = 8h..8h+7;
-// B supplies column l % 32, k = 8h..8h+7; the 16 accumulators of lane l hold column l % 32 and
-// rows 8g + 4h + r for g, r in 0..3 (acc[4g + r]).
+// MFMA 32x32x16 lane layout (per operand, lane l, h = l / 32): the first operand supplies row
+// l % 32, k = 8h..8h+7; the second supplies column l % 32, k = 8h..8h+7; the 16 accumulators of
+// lane l hold column l % 32 and rows 8g + 4h + r for g, r in 0..3 (acc[4g + r]). The k-loop
+// computes C^T = W . A^T (W first), so a lane ends up with 4 consecutive output columns of one
+// row per g: the epilogues convert them with packed instructions and store 8 or 16 bytes at once.
 //
 // Epilogues (fused, no extra pass over C):
 //   EPI_BF16   C bf16 = acc (+ bias) (then relu or gelu)
@@ -59,8 +60,15 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
   }
 }
 
-template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+// One BM x BN output tile: the k-loop over [kt0, kt0 + NK) and the epilogue.
+//
+// TR selects the MFMA operand order. TR: D = W . A^T, so a lane's 16 accumulators of a fragment
+// hold one output row (lane & 31) and columns 8g + 4h + r: four consecutive columns per g, stored
+// as one 8-byte (bf16) or 16-byte (f32) access after a packed conversion. !TR: D = A . W^T, a
+// lane holds one column and four consecutive rows per g; only the transposed v output of the
+// q|k|v epilogue ([H, 64, ldv], rows = tokens contiguous) wants that.
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0, int n0, int kt0, int NK, int split) {
   constexpr int NW = WM * WN;                // waves; each owns a TM x TN sub-tile
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;  // 32 x 32 MFMA fragments per wave
@@ -76,43 +84,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   static_assert(LPW * NW == AG + WG, "load groups must split evenly over the waves");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt range");
 
-  // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of ROWB bytes. The 16-byte chunk c
-  // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
-  // consecutive rows, the same k; 64 banks of 4 bytes) then hit 16 distinct 16-byte bank groups
-  // without padding, which the direct loads (whole 1 KiB runs) could not write.
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Tile order: each XCD takes a contiguous run of logical tiles (xcd_remap), and the run walks
-  // groups of GM row tiles across all column tiles, GM fastest. The ~32 workgroups an XCD holds
-  // at once then cover a GM x (32 / GM) patch, so its L2 serves every A row panel to many
-  // column tiles instead of re-reading the activations from HBM once per column tile.
-  constexpr int GM = BM >= 256 ? 4 : 8;
-  const int mt = (g.M + BM - 1) / BM;
-  const int nt = g.N / BN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int grp = bid / (GM * nt);
-  const int gm = min(GM, mt - grp * GM);
-  const int loc = bid - grp * GM * nt;
-  const int tile_m = grp * GM + loc % gm, tile_n = loc / gm;
-  const int m0 = tile_m * BM, n0 = tile_n * BN;
-  // This workgroup's k-tiles: [kt0, kt0 + NK) of the K / BK (split-K divides them evenly).
-  const int KT_ALL = g.K / BK;
-  const int split = blockIdx.y, S = gridDim.y;
-  const int kt0 = (split * KT_ALL) / S;
-  const int NK = ((split + 1) * KT_ALL) / S - kt0;
-
   // Global -> LDS without registers (global_load_lds_dwordx4): lane l of a load moves 16 bytes
   // of row l / CH of its RG-row group, chunk (l % CH) ^ swizzle, into slot l % CH.
   const int lrow = lane / CH, lslot = lane % CH;
-  auto issue = [&](int stage, int kt) {
+  // Loads j in [jlo, jhi) of this wave's LPW for k-tile kt into stage `stage`.
+  auto issue = [&](int stage, int kt, int jlo, int jhi) {
     char* sb = smem + stage * STAGE_BYTES;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
+      if (j < jlo || j >= jhi) continue;
       const int gi = wave + j * NW;
       if (gi < AG) {
         const int r = gi * RG + lrow;
@@ -138,7 +123,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < NK) issue(s, kt0 + s);
+    if (s < NK) issue(s, kt0 + s, 0, LPW);
 
   const int lr = lane & 31, lh = lane >> 5;
   for (int it = 0; it < NK; ++it) {
@@ -147,7 +132,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     // Every wave's loads of `it` have landed, and every wave is done with k-tile it - 1, whose
     // buffer the next issue overwrites.
     barrier_lds();
-    if (it + STAGES - 1 < NK) issue((it + STAGES - 1) % STAGES, kt0 + it + STAGES - 1);
+    // The next k-tile's loads go out over the first two k-steps of this one: issued as one burst
+    // they fill the address queue and stall the wave before its MFMAs (the two then do not
+    // overlap); issued later they have too little of the k-tile left to land in.
+    const bool pre = it + STAGES - 1 < NK;
+    const int pstage = (it + STAGES - 1) % STAGES, pkt = kt0 + it + STAGES - 1;
     const char* sa = smem + (it % STAGES) * STAGE_BYTES;
     const char* sw = sa + A_BYTES;
     bf16x8 af[2][FM], bw[2][FN];
@@ -164,144 +153,277 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       }
     };
     frag(0, 0);
+    constexpr int KS = BK / 16, LPK = (LPW + 1) / 2;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      if (ks + 1 < BK / 16) frag(ks + 1, (ks + 1) & 1);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (pre && ks < 2) issue(pstage, pkt, ks * LPK, min(LPW, (ks + 1) * LPK));
+      if (ks + 1 < KS) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bw[ks & 1][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (TR)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bw[ks & 1][j], acc[i][j], 0, 0, 0);
+        }
     }
   }
 
-  if (S > 1) {
-    // Split-K: this k-range's partial tile goes to ws[split] as f32; splitk_epilogue_kernel
-    // sums the splits and applies the epilogue.
-    float* part = g.ws + size_t(split) * g.M * g.N;
-    const int lh2 = lane >> 5;
+  const int l32 = lane & 31, h = lane >> 5;
+  constexpr int NT = NW * 64;
+  // bf16 results leave through LDS: after the k-loop the stage buffers are free, each wave
+  // writes its fragments there (8 bytes per lane, padded rows keep the 32 rows of one access on
+  // distinct banks), and the block then stores whole rows with 16-byte lane accesses, so every
+  // store instruction writes full cache lines instead of 16-byte pieces of 32 rows.
+  char* stg = smem;
+  if constexpr (!TR) {
+    // q|k|v epilogue, v blocks: columns [2d, 3d) go out transposed, [H, 64, ldv]. Lane holds
+    // column (lane & 31) of fragment 2p (dim i of a head; 2p + 1 has dim i + 32) and rows
+    // 8q + 4h .. + 3: 4 consecutive tokens of one dim, staged as [column][token].
+    static_assert(EPI == EPI_ROPE, "column-per-lane order is only used for the transposed v output");
+    constexpr int PV = BM * 2 + 8;
+    constexpr int NH = BN * PV <= STAGES * STAGE_BYTES ? 1 : 2;  // column halves staged one after the other
+    constexpr int HC = BN / NH;
+    static_assert(HC * PV <= STAGES * STAGE_BYTES && HC % 64 == 0, "v staging must fit the stage buffers");
+    const int head0 = (n0 - 2 * g.rope_d) >> 6;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = m0 + wm * TM + i * 32 + (e >> 2) * 8 + 4 * lh2 + (e & 3);
-          if (row < g.M) part[size_t(row) * g.N + n0 + wn * TN + j * 32 + (lane & 31)] = acc[i][j][e];
-        }
-    return;
-  }
-
-  // Epilogue. Lane holds column (lane & 31) and rows 8q + 4h + r of each 32x32 fragment.
-  const int h = lane >> 5;
-  const int colbase = n0 + wn * TN + (lane & 31);
-  const int rowbase = m0 + wm * TM + 4 * h;
-  if constexpr (EPI == EPI_GEGLU) {
-    uint16_t* C = reinterpret_cast<uint16_t*>(g.C);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int half = 0; half < NH; ++half) {
+      __syncthreads();
 #pragma unroll
       for (int p = 0; p < FN / 2; ++p) {
-        const int oc = (n0 + wn * TN) / 2 + p * 32 + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = rowbase + i * 32 + (e >> 2) * 8 + (e & 3);
-          if (row < g.M) {
-            const float x = acc[i][2 * p][e], gate = acc[i][2 * p + 1][e];
-            C[size_t(row) * g.ldc + oc] = f2bf(gelu_erf(x) * gate);
-          }
-        }
-      }
-  } else if constexpr (EPI == EPI_ROPE) {
-    // Columns [0, d) are q, [d, 2d) k, [2d, 3d) v; within a head of 64, dims i and i + 32 form a
-    // rotation pair. With TN a multiple of 64 and fragments of 32 columns, fragment 2p holds dim
-    // i = lane & 31 of a head and fragment 2p + 1 holds dim i + 32 of the same head, same rows.
-    // q and k go out as [H, T, 64]; v goes out transposed, [H, 64, ldv], which is the layout the
-    // attention kernel stages: a lane's 4 consecutive rows of one dim are one 8-byte store.
-    const int d = g.rope_d;
-    const int i = lane & 31;
-#pragma unroll
-    for (int p = 0; p < FN / 2; ++p) {
-      const int c0 = n0 + wn * TN + p * 64;  // first column of this head
-      const int part = c0 / d;                 // 0 q, 1 k, 2 v
-      const int head = (c0 - part * d) >> 6;
-      if (part == 2) {
-        uint16_t* v1 = g.rope_v + (size_t(head) * 64 + i) * g.rope_ldv;
-        uint16_t* v2 = v1 + size_t(32) * g.rope_ldv;
-        const float b1 = g.bias ? g.bias[c0 + i] : 0.0f, b2 = g.bias ? g.bias[c0 + 32 + i] : 0.0f;
+        const int cl = wn * TN + p * 64 + l32;
+        if ((wn * TN + p * 64) / HC != half) continue;
+        const float b1 = g.bias ? g.bias[n0 + cl] : 0.0f, b2 = g.bias ? g.bias[n0 + cl + 32] : 0.0f;
+        char* col1 = stg + (cl - half * HC) * PV;
+        char* col2 = col1 + 32 * PV;
 #pragma unroll
         for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const int row = rowbase + mi * 32 + q4 * 8;  // 4 rows row .. row + 3
+            const int rl = wm * TM + mi * 32 + q4 * 8 + 4 * h;
             const f32x16& a1 = acc[mi][2 * p];
             const f32x16& a2 = acc[mi][2 * p + 1];
-            if (row + 3 < g.M) {
-              *reinterpret_cast<uint2*>(v1 + row) = make_uint2(pack2(a1[q4 * 4 + 0] + b1, a1[q4 * 4 + 1] + b1),
-                                                               pack2(a1[q4 * 4 + 2] + b1, a1[q4 * 4 + 3] + b1));
-              *reinterpret_cast<uint2*>(v2 + row) = make_uint2(pack2(a2[q4 * 4 + 0] + b2, a2[q4 * 4 + 1] + b2),
-                                                               pack2(a2[q4 * 4 + 2] + b2, a2[q4 * 4 + 3] + b2));
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (row + r < g.M) {
-                  v1[row + r] = f2bf(a1[q4 * 4 + r] + b1);
-                  v2[row + r] = f2bf(a2[q4 * 4 + r] + b2);
-                }
-            }
+            *reinterpret_cast<uint2*>(col1 + rl * 2) =
+                make_uint2(pack2(a1[q4 * 4] + b1, a1[q4 * 4 + 1] + b1), pack2(a1[q4 * 4 + 2] + b1, a1[q4 * 4 + 3] + b1));
+            *reinterpret_cast<uint2*>(col2 + rl * 2) =
+                make_uint2(pack2(a2[q4 * 4] + b2, a2[q4 * 4 + 1] + b2), pack2(a2[q4 * 4 + 2] + b2, a2[q4 * 4 + 3] + b2));
           }
-        continue;
       }
-      uint16_t* dst = part == 0 ? g.rope_q : g.rope_k;
-      const float b1 = g.bias ? g.bias[c0 + i] : 0.0f, b2 = g.bias ? g.bias[c0 + 32 + i] : 0.0f;
-#pragma unroll
-      for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = rowbase + mi * 32 + (e >> 2) * 8 + (e & 3);
-          if (row < g.M) {
-            float x1 = acc[mi][2 * p][e] + b1, x2 = acc[mi][2 * p + 1][e] + b2;
-            if (g.rope_cos) {
-              const int pos = g.rope_pos[row];
-              const float c = g.rope_cos[pos * 32 + i], s = g.rope_sin[pos * 32 + i];
-              const float y1 = x1 * c - x2 * s;
-              x2 = x1 * s + x2 * c;
-              x1 = y1;
-            }
-            uint16_t* o = dst + (size_t(head) * g.rope_T + row) * 64;
-            o[i] = f2bf(x1);
-            o[i + 32] = f2bf(x2);
-          }
+      __syncthreads();
+      for (int idx = tid; idx < HC * (BM / 8); idx += NT) {
+        const int c = idx / (BM / 8), k8 = idx % (BM / 8);
+        const int tok = m0 + k8 * 8;
+        if (tok >= g.M) continue;
+        const int cg = half * HC + c;  // column within the tile
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + c * PV + k8 * 16);
+        uint16_t* dst = g.rope_v + (size_t(head0 + cg / 64) * 64 + cg % 64) * g.rope_ldv + tok;
+        if (tok + 8 <= g.M) {
+          *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+          for (int e = 0; e < g.M - tok; ++e) dst[e] = uint16_t(w[e >> 1] >> (16 * (e & 1)));
         }
+      }
     }
+    return;
   } else {
+    // Lane holds row rbase + 32 i and columns cbase + 32 j + 8 q .. + 3 (acc[i][j][4 q + r]).
+    const int rbase = m0 + wm * TM + l32;
+    const int cbase = n0 + wn * TN + 4 * h;
+    const int rl0 = wm * TM + l32;        // the same row and column, local to the tile
+    const int cl0 = wn * TN + 4 * h;
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (g.splits > 1) {
+      // Split-K: this k-range's partial tile goes to ws[split] as f32; splitk_epilogue_kernel
+      // sums the splits and applies the epilogue.
+      float* part = g.ws + size_t(split) * g.M * g.N;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = colbase + j * 32;
-      const float bias = g.bias ? g.bias[col] : 0.0f;
+      for (int i = 0; i < FM; ++i) {
+        const int row = rbase + i * 32;
+        if (row >= g.M) continue;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = rowbase + i * 32 + (e >> 2) * 8 + (e & 3);
-          if (row < g.M) {
-            float v = acc[i][j][e] + bias;
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4*>(part + size_t(row) * g.N + cbase + j * 32 + q * 8) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+      }
+      return;
+    }
+    if constexpr (EPI == EPI_RESID || EPI == EPI_F32) {
+      // f32 C (+)= acc + bias, 16 bytes per lane access.
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = cbase + j * 32 + q * 8;
+          const float4 b = g.bias ? *reinterpret_cast<const float4*>(g.bias + col) : zero4;
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            const int row = rbase + i * 32;
+            if (row >= g.M) continue;
+            float4* c = reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + size_t(row) * g.ldc + col);
+            const float4 v = make_float4(acc[i][j][4 * q] + b.x, acc[i][j][4 * q + 1] + b.y,
+                                         acc[i][j][4 * q + 2] + b.z, acc[i][j][4 * q + 3] + b.w);
             if constexpr (EPI == EPI_RESID) {
-              float* C = reinterpret_cast<float*>(g.C);
-              C[size_t(row) * g.ldc + col] += v;
-            } else if constexpr (EPI == EPI_F32) {
-              float* C = reinterpret_cast<float*>(g.C);
-              C[size_t(row) * g.ldc + col] = v;
+              const float4 old = *c;
+              *c = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
             } else {
-              if (g.act == ACT_RELU) v = fmaxf(v, 0.0f);
-              else if (g.act == ACT_GELU) v = gelu_erf(v);
-              uint16_t* C = reinterpret_cast<uint16_t*>(g.C);
-              C[size_t(row) * g.ldc + col] = f2bf(v);
+              *c = v;
             }
           }
         }
+      return;
+    } else if constexpr (EPI == EPI_GEGLU) {
+      // W rows interleaved by 32: fragment 2p is x, 2p + 1 its gate; output columns
+      // (n0 + wn TN) / 2 + 32 p + 8 q + 4 h .. + 3. Stored directly (8 bytes per lane): the
+      // half-width rows gain less from LDS staging than its two barriers cost.
+      uint16_t* C = reinterpret_cast<uint16_t*>(g.C);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = rbase + i * 32;
+        if (row >= g.M) continue;
+        uint16_t* crow = C + size_t(row) * g.ldc + (n0 + wn * TN) / 2 + 4 * h;
+#pragma unroll
+        for (int p = 0; p < FN / 2; ++p)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16& x = acc[i][2 * p];
+            const f32x16& gt = acc[i][2 * p + 1];
+            *reinterpret_cast<uint2*>(crow + p * 32 + q * 8) =
+                make_uint2(pack2(gelu_erf(x[4 * q]) * gt[4 * q], gelu_erf(x[4 * q + 1]) * gt[4 * q + 1]),
+                           pack2(gelu_erf(x[4 * q + 2]) * gt[4 * q + 2], gelu_erf(x[4 * q + 3]) * gt[4 * q + 3]));
+          }
+      }
+    } else {
+      // Staged bf16 tile [BM][BN], in row halves when the whole tile does not fit.
+      constexpr int P = BN * 2 + 8;
+      constexpr int NH = BM * P <= STAGES * STAGE_BYTES ? 1 : 2;
+      constexpr int HR = BM / NH;
+      static_assert(HR * P <= STAGES * STAGE_BYTES && HR % 32 == 0, "output staging must fit the stage buffers");
+      int pos[FM];
+      if constexpr (EPI == EPI_ROPE) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) pos[i] = g.rope_cos ? g.rope_pos[min(rbase + i * 32, g.M - 1)] : 0;
+      }
+#pragma unroll
+      for (int half = 0; half < NH; ++half) {
+        __syncthreads();
+        if constexpr (EPI == EPI_ROPE) {
+          // q and k blocks: columns [0, d) q, [d, 2d) k; within a head of 64, dims i and i + 32
+          // form a rotation pair. Fragment 2p holds dims 0..31 of a head and 2p + 1 dims 32..63,
+          // so a lane has dims i0 .. i0 + 3 (i0 = 8 q + 4 h) and their partners, same row.
+#pragma unroll
+          for (int p = 0; p < FN / 2; ++p) {
+            const int c0 = n0 + wn * TN + p * 64;  // first column of this head
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int i0 = q * 8 + 4 * h;
+              const float4 b1 = g.bias ? *reinterpret_cast<const float4*>(g.bias + c0 + i0) : zero4;
+              const float4 b2 = g.bias ? *reinterpret_cast<const float4*>(g.bias + c0 + 32 + i0) : zero4;
+#pragma unroll
+              for (int i = 0; i < FM; ++i) {
+                if ((wm * TM + i * 32) / HR != half) continue;
+                const f32x16& a1 = acc[i][2 * p];
+                const f32x16& a2 = acc[i][2 * p + 1];
+                float x1[4] = {a1[4 * q] + b1.x, a1[4 * q + 1] + b1.y, a1[4 * q + 2] + b1.z, a1[4 * q + 3] + b1.w};
+                float x2[4] = {a2[4 * q] + b2.x, a2[4 * q + 1] + b2.y, a2[4 * q + 2] + b2.z, a2[4 * q + 3] + b2.w};
+                if (g.rope_cos) {
+                  const float4 c4 = *reinterpret_cast<const float4*>(g.rope_cos + pos[i] * 32 + i0);
+                  const float4 s4 = *reinterpret_cast<const float4*>(g.rope_sin + pos[i] * 32 + i0);
+                  const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                  for (int r = 0; r < 4; ++r) {
+                    const float y1 = x1[r] * cs[r] - x2[r] * sn[r];
+                    x2[r] = x1[r] * sn[r] + x2[r] * cs[r];
+                    x1[r] = y1;
+                  }
+                }
+                char* o = stg + (rl0 + i * 32 - half * HR) * P + (c0 - n0 + i0) * 2;
+                *reinterpret_cast<uint2*>(o) = make_uint2(pack2(x1[0], x1[1]), pack2(x1[2], x1[3]));
+                *reinterpret_cast<uint2*>(o + 64) = make_uint2(pack2(x2[0], x2[1]), pack2(x2[2], x2[3]));
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float4 b = g.bias ? *reinterpret_cast<const float4*>(g.bias + cbase + j * 32 + q * 8) : zero4;
+#pragma unroll
+              for (int i = 0; i < FM; ++i) {
+                if ((wm * TM + i * 32) / HR != half) continue;
+                float v[4] = {acc[i][j][4 * q] + b.x, acc[i][j][4 * q + 1] + b.y, acc[i][j][4 * q + 2] + b.z,
+                              acc[i][j][4 * q + 3] + b.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  if (g.act == ACT_RELU) v[r] = fmaxf(v[r], 0.0f);
+                  else if (g.act == ACT_GELU) v[r] = gelu_erf(v[r]);
+                }
+                *reinterpret_cast<uint2*>(stg + (rl0 + i * 32 - half * HR) * P + (cl0 + j * 32 + q * 8) * 2) =
+                    make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+              }
+            }
+        }
+        __syncthreads();
+        // Whole rows out: 16 bytes per lane, BN / 8 lanes per row.
+        for (int idx = tid; idx < HR * (BN / 8); idx += NT) {
+          const int r = idx / (BN / 8), c8 = idx % (BN / 8);
+          const int row = m0 + half * HR + r;
+          if (row >= g.M) continue;
+          const uint4 v = *reinterpret_cast<const uint4*>(stg + r * P + c8 * 16);
+          uint16_t* dst;
+          if constexpr (EPI == EPI_ROPE) {
+            const int c0 = n0 + (c8 / 8) * 64;
+            const int part = c0 / g.rope_d;  // 0 q, 1 k
+            const int head = (c0 - part * g.rope_d) >> 6;
+            dst = (part == 0 ? g.rope_q : g.rope_k) + (size_t(head) * g.rope_T + row) * 64 + (c8 % 8) * 8;
+          } else {
+            dst = reinterpret_cast<uint16_t*>(g.C) + size_t(row) * g.ldc + n0 + c8 * 8;
+          }
+          *reinterpret_cast<uint4*>(dst) = v;
+        }
+      }
     }
   }
+}
+
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+  // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of BK * 2 bytes. The 16-byte chunk c
+  // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
+  // consecutive rows, the same k; 64 banks of 4 bytes) then hit 16 distinct 16-byte bank groups
+  // without padding, which the direct loads (whole 1 KiB runs) could not write.
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * (BM + BN) * BK * 2];
+
+  // Tile order: each XCD takes a contiguous run of logical tiles (xcd_remap), and the run walks
+  // groups of GM row tiles across all column tiles, GM fastest. The ~32 workgroups an XCD holds
+  // at once then cover a GM x (32 / GM) patch, so its L2 serves every A row panel to many
+  // column tiles instead of re-reading the activations from HBM once per column tile.
+  constexpr int GM = BM >= 256 ? 4 : 8;
+  const int mt = (g.M + BM - 1) / BM;
+  const int nt = g.N / BN;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int grp = bid / (GM * nt);
+  const int gm = min(GM, mt - grp * GM);
+  const int loc = bid - grp * GM * nt;
+  const int tile_m = grp * GM + loc % gm, tile_n = loc / gm;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  // This workgroup's k-tiles: [kt0, kt0 + NK) of the K / BK (split-K divides them evenly).
+  const int KT_ALL = g.K / BK;
+  const int split = blockIdx.y, S = gridDim.y;
+  const int kt0 = (split * KT_ALL) / S;
+  const int NK = ((split + 1) * KT_ALL) / S - kt0;
+
+  if constexpr (EPI == EPI_ROPE) {
+    if (n0 >= 2 * g.rope_d) {
+      gemm_tile<BM, BN, BK, STAGES, WM, WN, EPI, false>(g, smem, m0, n0, kt0, NK, split);
+      return;
+    }
+  }
+  gemm_tile<BM, BN, BK, STAGES, WM, WN, EPI, true>(g, smem, m0, n0, kt0, NK, split);
 }
 
 template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
@@ -311,12 +433,17 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
                      st, g);
 }
 
+// Tile configurations. Small M (one request of up to ~1000 tokens, the decision head's picked
+// rows): 64 x 128 tiles in 4 waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two
+// workgroups per CU); these GEMMs stream their weights, so load depth matters more than operand
+// reuse. Large M: 128 x 128 tiles in 4 waves of 64 x 64, two stages (64 KiB, two per CU).
+constexpr int SMALL_M = 1024;
+inline int tile_m_of(int M) { return M <= SMALL_M ? 64 : 128; }
+
 template <int EPI>
 void launch_e(const GemmArgs& g, hipStream_t st) {
-  // 64-row tiles for tiny M; otherwise 128 x 128 with two k-tiles in LDS (64 KiB), which lets
-  // two workgroups share a CU (two waves per SIMD).
-  if (g.M <= 64)
-    launch_t<64, 128, 64, 2, 1, 2, EPI>(g, st);
+  if (g.M <= SMALL_M)
+    launch_t<64, 128, 64, 3, 2, 2, EPI>(g, st);
   else
     launch_t<128, 128, 64, 2, 2, 2, EPI>(g, st);
 }
@@ -397,13 +524,14 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
 
 GemmPlan gemm_plan(int M, int N, int K) {
   GemmPlan p;
-  const int bm = M <= 64 ? 64 : 128;
+  const int bm = tile_m_of(M);
   const int tiles = ((M + bm - 1) / bm) * (N / 128);
   const int KT = K / BK;
-  // Few tiles (small M): split K so the workgroups cover the 256 CUs about twice, each keeping
-  // at least 2 k-tiles.
+  // Few tiles (a short request on a narrow output): split K so that about 256 workgroups run,
+  // each keeping at least 4 k-tiles, and the f32 partials (s M N 4 bytes, written and read
+  // back) stay within twice the weight bytes (N K 2) the GEMM streams anyway.
   int s = 1;
-  if (tiles < 192) s = std::max(1, std::min(KT / 2, (512 + tiles - 1) / tiles));
+  if (tiles < 96) s = std::max(1, std::min({KT / 4, (256 + tiles - 1) / tiles, K / std::max(M, 1)}));
   p.splits = s;
   p.ws_floats = s > 1 ? size_t(s) * M * N : 0;
   return p;
@@ -418,6 +546,16 @@ const char* gemm_check(const GemmArgs& g) {
   if (g.epi == EPI_ROPE && (g.rope_ldv % 8 || g.rope_ldv < g.M + 64)) return "gemm: v row stride must be a multiple of 8 and >= M + 64";
   if (g.splits < 1 || g.splits > g.K / BK) return "gemm: splits must be in 1..K/64";
   if (g.splits > 1 && !g.ws) return "gemm: split-K needs a workspace";
+  // The epilogues store 4 consecutive columns per access (8 bytes bf16, 16 bytes f32) and read
+  // bias and RoPE tables 4 floats at a time.
+  auto mis = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; };
+  const bool f32out = g.epi == EPI_RESID || g.epi == EPI_F32;
+  if (g.epi != EPI_ROPE && ((g.ldc % (f32out ? 4 : 8)) || mis(g.C, 16)))
+    return "gemm: C must be 16-byte aligned with 16-byte row strides";
+  if (mis(g.bias, 16) || mis(g.ws, 16)) return "gemm: bias and workspace must be 16-byte aligned";
+  if (g.epi == EPI_ROPE && (mis(g.rope_q, 16) || mis(g.rope_k, 16) || mis(g.rope_v, 16) || mis(g.rope_cos, 16) ||
+                            mis(g.rope_sin, 16)))
+    return "gemm: q, k, v and the RoPE tables must be 16-byte aligned";
   return nullptr;
 }
 
