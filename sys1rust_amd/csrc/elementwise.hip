@@ -9,6 +9,19 @@ namespace s1 {
 
 namespace {
 
+// 8 consecutive floats as two 16-byte loads (parameters are read this way, not element by
+// element: scalar loads each wait for the previous one and serialise the row on L2 latency).
+__device__ __forceinline__ void load8f(const float* __restrict__ p, float* f) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+__device__ __forceinline__ void store8f(float* p, const float* f) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(f[0], f[1], f[2], f[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(f[4], f[5], f[6], f[7]);
+}
+
 // Row statistics of a wave-owned row of PL*64 floats held as v[PL] per lane.
 template <int PL>
 __device__ __forceinline__ void ln_stats(const float* v, int d, float eps, float& mean, float& rstd) {
@@ -43,15 +56,16 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restric
   }
   float mean, rstd;
   ln_stats<PL>(v, d, eps, mean, rstd);
+  float wv[PL];
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) load8f(w + c * 512 + lane * 8, wv + c * 8);
 #pragma unroll
   for (int c = 0; c < PL / 8; ++c) {
     const int o = c * 512 + lane * 8;
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (v[c * 8 + e] - mean) * rstd * w[o + e];
-    float4* hp = reinterpret_cast<float4*>(h + size_t(row) * d + o);
-    hp[0] = make_float4(y[0], y[1], y[2], y[3]);
-    hp[1] = make_float4(y[4], y[5], y[6], y[7]);
+    for (int e = 0; e < 8; ++e) y[e] = (v[c * 8 + e] - mean) * rstd * wv[c * 8 + e];
+    store8f(h + size_t(row) * d + o, y);
     *reinterpret_cast<uint4*>(x + size_t(row) * d + o) = pack8(y);
   }
 }
@@ -75,31 +89,40 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     v[c * 8 + 0] = a.x; v[c * 8 + 1] = a.y; v[c * 8 + 2] = a.z; v[c * 8 + 3] = a.w;
     v[c * 8 + 4] = bq.x; v[c * 8 + 5] = bq.y; v[c * 8 + 6] = bq.z; v[c * 8 + 7] = bq.w;
   }
+  // Parameters for this lane's elements, loaded while the row statistics reduce.
+  float wv[PL], bv[PL];
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) load8f(w + c * 512 + lane * 8, wv + c * 8);
+  if (b) {
+#pragma unroll
+    for (int c = 0; c < PL / 8; ++c) load8f(b + c * 512 + lane * 8, bv + c * 8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) bv[i] = 0.0f;
+  }
   float mean, rstd;
   ln_stats<PL>(v, d, eps, mean, rstd);
-  const float* av = addv ? addv + size_t(seg[row]) * d : nullptr;
+  float y[PL];
 #pragma unroll
-  for (int c = 0; c < PL / 8; ++c) {
-    const int o = c * 512 + lane * 8;
-    float y[8];
+  for (int i = 0; i < PL; ++i) y[i] = (v[i] - mean) * rstd * wv[i] + bv[i];
+  if (yb) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      y[e] = (v[c * 8 + e] - mean) * rstd * w[o + e];
-      if (b) y[e] += b[o + e];
-    }
-    if (yb) *reinterpret_cast<uint4*>(yb + size_t(row) * d + o) = pack8(y);
-    if (yf) {
-      float4* hp = reinterpret_cast<float4*>(yf + size_t(row) * d + o);
-      hp[0] = make_float4(y[0], y[1], y[2], y[3]);
-      hp[1] = make_float4(y[4], y[5], y[6], y[7]);
-    }
-    if (yplus) {
+    for (int c = 0; c < PL / 8; ++c)
+      *reinterpret_cast<uint4*>(yb + size_t(row) * d + c * 512 + lane * 8) = pack8(y + c * 8);
+  }
+  if (yf) {
+#pragma unroll
+    for (int c = 0; c < PL / 8; ++c) store8f(yf + size_t(row) * d + c * 512 + lane * 8, y + c * 8);
+  }
+  if (yplus) {
+    const float* av = addv + size_t(seg[row]) * d;
+#pragma unroll
+    for (int c = 0; c < PL / 8; ++c) {
       float z[8];
+      load8f(av + c * 512 + lane * 8, z);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) z[e] = y[e] + av[o + e];
-      float4* hp = reinterpret_cast<float4*>(yplus + size_t(row) * d + o);
-      hp[0] = make_float4(z[0], z[1], z[2], z[3]);
-      hp[1] = make_float4(z[4], z[5], z[6], z[7]);
+      for (int e = 0; e < 8; ++e) z[e] += y[c * 8 + e];
+      store8f(yplus + size_t(row) * d + c * 512 + lane * 8, z);
     }
   }
 }
@@ -198,10 +221,11 @@ __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict_
   if (row >= R) return;
   float acc = 0.0f;
   for (int o = lane * 8; o < d; o += 512) {
-    float v[8];
+    float v[8], wv[8];
     unpack8(*reinterpret_cast<const uint4*>(x + size_t(row) * d + o), v);
+    load8f(w + o, wv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += v[e] * w[o + e];
+    for (int e = 0; e < 8; ++e) acc += v[e] * wv[e];
   }
   acc = wave_sum(acc);
   if (lane == 0) out[row] = acc + (b ? b[0] : 0.0f);
