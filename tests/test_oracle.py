@@ -69,6 +69,32 @@ def test_oracle_matches_golden_modernbert_large():
     assert dp < POOLED_REL_TOL, dp
 
 
+@pytest.mark.parametrize("case", ["golden_small", "golden_large"])
+def test_torch_restatement_matches_oracle_and_golden(case):
+    """oracle/torch_ref.py (the checker for the 8192-token and 64-request GPU cases) performs
+    the oracle's steps in torch: it must meet the golden fixtures at the oracle's own tolerances
+    and agree with the numpy oracle to float32 rounding."""
+    import torch
+
+    from oracle.torch_ref import TorchOracle
+
+    z, cfg, agent, b, st = load_case(case)
+    o = O.Oracle(st, cfg, agent)
+    t = TorchOracle(o, "cpu")
+    with torch.no_grad():
+        rel, dl, dp = compare(z, t, b)
+    assert rel < HIDDEN_REL_TOL, rel
+    assert dl < LOGIT_ABS_TOL, dl
+    assert dp < POOLED_REL_TOL, dp
+    enc_t, enc_o = t.encoder_hidden(b), o.encoder_hidden(b)
+    am = b.attention_mask.reshape(b.n, b.len).astype(bool)
+    d = np.linalg.norm(enc_t[am] - enc_o[am], axis=-1) / np.linalg.norm(enc_o[am], axis=-1)
+    assert float(d.max()) < 2e-5, float(d.max())
+    lt, _ = t.forward(b, enc_o)
+    lo, _ = o.forward(b, enc_o)
+    assert float(np.abs(lt - lo).max()) < 1e-5
+
+
 @pytest.mark.parametrize("mistake", ["window+1", "theta_swap", "geglu_order", "head_scale", "drop_out_proj_bias",
                                      "emb_norm_weight_dropped", "rope_traditional"])
 def test_planted_mistakes_fail_the_golden_check(small, mistake, monkeypatch):
