@@ -114,6 +114,17 @@ def main() -> int:
     shapes[args.workload] = round(ms, 4)
     print(f"[bench] {args.workload}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
 
+    # Throughput context (not the metric): the 64-request varlen sweep packed into one forward,
+    # and one 8192-token state.
+    throughput = {}
+    for name in ([] if args.no_context else ["sweep64", "state8192_1q"]):
+        tb = workload(name, seed=args.seed)
+        tms, _ = run(tb, 3, 1)
+        throughput[name] = {"ms_per_batch": round(tms, 3), "rows": tb.n, "tokens": tb.total_tokens(),
+                            "sequences_per_s": round(tb.n / (tms * 1e-3), 1),
+                            "tokens_per_s": round(tb.total_tokens() / (tms * 1e-3))}
+        print(f"[bench] {name}: {tms:.2f} ms for {tb.n} rows, {tb.total_tokens()} tokens", file=sys.stderr, flush=True)
+
     # Kernel timing: the same steps on a second instance with the `ops` setting, which records a
     # HIP event pair around every launch on the model's stream (and so runs without graphs).
     kmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in ["ops", args.settings] if x))
@@ -138,6 +149,16 @@ def main() -> int:
     dk = gemms[dom]
     gemm_flop_step = sum(gemm_flops(k, T, P, R, d, I, SCORER_WIDTH) * v["launches"] / args.steps for k, v in gemms.items())
     gemm_ms_step = sum(v["total_ms_per_step"] for v in gemms.values())
+    # HBM bytes per launch of the dominant kernel come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    # (they cannot be read from inside this process); the measured figure is kept with its
+    # provenance in profiles/traffic.json and reported when it is for this kernel and workload.
+    traffic, traffic_src = None, None
+    tj = ROOT / "profiles" / "traffic.json"
+    if tj.exists():
+        tr = json.loads(tj.read_text())
+        if tr.get("kernel") == dom and tr.get("workload", "").startswith(args.workload):
+            traffic = tr["hbm_bytes_per_launch"]
+            traffic_src = f"{tr['source']}; library commit {tr['library_commit']}"
     roofline = {
         "kernel": dom,
         "bound": "mfma",
@@ -145,10 +166,12 @@ def main() -> int:
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(dk["tflops"] / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
         "flop_per_launch": gemm_flops(dom, T, P, R, d, I, SCORER_WIDTH),
         "avg_launch_us": dk["avg_us"],
         "all_encoder_gemms_tflops": round(gemm_flop_step / (gemm_ms_step * 1e-3) / 1e12, 1),
+        "traffic_unit": "bytes per launch",
+        "traffic_source": traffic_src,
         "measured": f"HIP events around every launch on the model's stream over {args.steps} steps of the "
                     f"workload ({ms_eager:.3f} ms/request in that region)",
     }
@@ -199,6 +222,7 @@ def main() -> int:
                    "rows": b.n, "tokens": T, "padded_len": b.len, "seed": args.seed},
         "sequences_per_s": round(b.n / (ms * 1e-3), 1),
         "shapes_ms_per_request": shapes,
+        "throughput": throughput,
         "gemm_mfma_util": {k: v["mfma_util"] for k, v in gemms.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -22,7 +22,7 @@ from oracle import oracle as O
 from sys1rust_amd.backend import HipBackend, synth_checkpoint
 from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, Batch, workload
 
-from gates import check_answers, hidden_rel, say
+from gates import HIDDEN_REL_GATE, PROB_ABS_GATE, check_answers, hidden_rel, say
 
 pytestmark = pytest.mark.gpu
 
