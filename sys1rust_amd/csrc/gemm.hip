@@ -433,19 +433,31 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
                      st, g);
 }
 
-// Tile configurations. Small M (one request of up to ~1000 tokens, the decision head's picked
-// rows): 64 x 128 tiles in 4 waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two
-// workgroups per CU); these GEMMs stream their weights, so load depth matters more than operand
-// reuse. Large M: 128 x 128 tiles in 4 waves of 64 x 64, two stages (64 KiB, two per CU).
+// Tile configurations, chosen from the number of 128 x 128 tiles the GEMM has (the GPU holds
+// two workgroups on each of its 256 CUs):
+//   small  (one request of up to ~1000 tokens, or fewer than 200 tiles): 64 x 128 tiles in 4
+//          waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two workgroups per CU);
+//          these GEMMs stream their weights, so load depth matters more than operand reuse;
+//   mid    (fewer than 700 tiles, e.g. the 1024-wide Wo / Wo2 at a 10-question request): the same
+//          64 x 128 tiles, two stages; twice the tiles spread evenly over the CUs where 128-row
+//          tiles leave most CUs one tile and some two;
+//   large  128 x 128 tiles in 4 waves of 64 x 64, two stages (64 KiB, two per CU).
 constexpr int SMALL_M = 1024;
-inline int tile_m_of(int M) { return M <= SMALL_M ? 64 : 128; }
+enum TileCfg { TC_SMALL, TC_MID, TC_LARGE };
+inline TileCfg tile_cfg(int M, int N) {
+  if (M <= SMALL_M) return TC_SMALL;
+  const long long t128 = (long long)((M + 127) / 128) * (N / 128);
+  return t128 < 200 ? TC_SMALL : t128 < 700 ? TC_MID : TC_LARGE;
+}
+inline int tile_m_of(int M, int N) { return tile_cfg(M, N) == TC_LARGE ? 128 : 64; }
 
 template <int EPI>
 void launch_e(const GemmArgs& g, hipStream_t st) {
-  if (g.M <= SMALL_M)
-    launch_t<64, 128, 64, 3, 2, 2, EPI>(g, st);
-  else
-    launch_t<128, 128, 64, 2, 2, 2, EPI>(g, st);
+  switch (tile_cfg(g.M, g.N)) {
+    case TC_SMALL: launch_t<64, 128, 64, 3, 2, 2, EPI>(g, st); break;
+    case TC_MID: launch_t<64, 128, 64, 2, 2, 2, EPI>(g, st); break;
+    case TC_LARGE: launch_t<128, 128, 64, 2, 2, 2, EPI>(g, st); break;
+  }
 }
 
 // Sum of the split-K partials in split order, then the GEMM's epilogue. One thread per row and
@@ -524,7 +536,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
 
 GemmPlan gemm_plan(int M, int N, int K) {
   GemmPlan p;
-  const int bm = tile_m_of(M);
+  const int bm = tile_m_of(M, N);
   const int tiles = ((M + bm - 1) / bm) * (N / 128);
   const int KT = K / BK;
   // Few tiles (a short request on a narrow output): split K so that about 256 workgroups run,
