@@ -46,7 +46,8 @@ void attn_kernel(AttnArgs a) {
 
   const AttnTile tl = a.tiles[blockIdx.x];
   const int head = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int hl = lane >> 5;   // lane half
   const int col = lane & 31;  // query column within the wave
 
@@ -259,14 +260,204 @@ void attn_kernel(AttnArgs a) {
     }
 }
 
+// Local layers with a window of at most 64 keys: a workgroup's 128 queries see at most
+// 128 + 2 * 64 keys, so the whole key range is staged in LDS at once (every load of the
+// workgroup in flight together, one barrier) and each wave then runs its queries' softmax over
+// its own window in a single pass (at most 6 tiles of 32 keys, raw logits kept in registers).
+constexpr int LQ = 128;                 // queries per workgroup: 4 waves x 32
+constexpr int LMAXW = 64;               // largest window this kernel stages
+constexpr int LMAXK = LQ + 2 * LMAXW + 8;  // staged keys: the range plus 8-alignment slack
+constexpr int LKW = 72;                 // K row in LDS (bf16): 36 words, 16 rows per 16-byte phase on distinct banks
+// V^T row in LDS (bf16): 146 words (2 x odd), so the 32 lanes' 8-byte reads of one access hit
+// 64 distinct banks; 292 >= LMAXK rounded up to 32 keys, the furthest column a tile reads.
+constexpr int LVW = 292;
+constexpr int LTILES = (32 + 2 * LMAXW + 7 + 31) / 32;  // 32-key tiles a wave's window spans
+constexpr int LG = (LMAXK + 31) / 32 * 4;  // V^T 8-key groups per dim row staged or zeroed (36)
+constexpr int LPIECES = (LMAXK * 8 + 64 * LG + 255) / 256;  // 16-byte pieces per thread
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_local_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[LMAXK * LKW];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[64 * LVW];
+
+  const AttnTile tl = a.tiles[blockIdx.x];
+  const int head = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Wave-uniform values go through readfirstlane so the branches on them are scalar branches,
+  // not exec-mask regions around every tile.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5, col = lane & 31;
+  const int W = a.window;
+
+  const uint16_t* __restrict__ Qh = a.q + size_t(head) * a.Tq * 64;
+  const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.Tk * 64;
+  const uint16_t* __restrict__ Vt = a.v + size_t(head) * 64 * a.ldv;
+
+  // The workgroup's keys [kb0, kb1), staged from the 8-aligned cstart (keys below kb0 are masked
+  // out of S; V entries from kb1 on are zeroed, since the v buffer's slack is not initialised).
+  const int kb0 = max(tl.k0, tl.q0 - W), kb1 = min(tl.k1, tl.q1 + W);
+  const int cstart = kb0 & ~7;
+  const int nk8 = (kb1 - cstart + 7) >> 3;  // 8-key groups staged (<= LMAXK / 8)
+  const int lim = nk8 * 8;                  // staged keys
+  const int ng = ((lim + 31) & ~31) / 8;    // V^T groups staged (< nk8) or zeroed, up to 32-key multiple
+  const int kp = nk8 * 64;                  // K pieces: 8 per key
+  const int np = kp + 64 * LG;              // + V^T slots: 64 dims x LG groups (those >= ng idle)
+  {
+    uint4 st[LPIECES];
+#pragma unroll
+    for (int it = 0; it < LPIECES; ++it) {
+      const int p = tid + it * 256;
+      if (p < kp) {
+        const int key = p >> 3, dc = (p & 7) * 8;
+        st[it] = *reinterpret_cast<const uint4*>(Kh + size_t(min(cstart + key, kb1 - 1)) * 64 + dc);
+      } else if (p < np) {
+        const int q = p - kp;
+        const int dim = q / LG, g8 = q - dim * LG;
+        if (g8 >= nk8) {  // past the staged keys: zero (only the groups below ng are stored)
+          st[it] = make_uint4(0, 0, 0, 0);
+          continue;
+        }
+        const int c = cstart + g8 * 8;
+        uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c);
+        const int valid = kb1 - c;
+        if (valid < 8) {
+          uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          v = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        st[it] = v;
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < LPIECES; ++it) {
+      const int p = tid + it * 256;
+      if (p < kp) {
+        *reinterpret_cast<uint4*>(&sK[(p >> 3) * LKW + (p & 7) * 8]) = st[it];
+      } else if (p < np) {
+        const int q = p - kp;
+        const int dim = q / LG, g8 = q - dim * LG;
+        if (g8 < ng) *reinterpret_cast<uint4*>(&sVt[dim * LVW + g8 * 8]) = st[it];
+      }
+    }
+  }
+  __syncthreads();
+
+  const int wq0 = tl.q0 + wave * 32;
+  if (wq0 >= tl.q1) return;  // no barrier follows
+  const int qi = wq0 + col;
+  const bool qvalid = qi < tl.q1;
+  const int qk = min(qi, tl.q1 - 1);
+  bf16x8 qf[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+
+  // This wave's window: keys [ws, we) cover every query's |key - q| <= W within the row.
+  const int ws = max(kb0, wq0 - W), we = min(kb1, min(wq0 + 31, tl.q1 - 1) + W + 1);
+  int t0 = (ws - cstart) & ~7;                 // LDS key offset of the first tile
+  const int nt = __builtin_amdgcn_readfirstlane((we - cstart - t0 + 31) >> 5);  // tiles to visit (<= LTILES)
+  // Shift the tiles left so they end within the staged keys (keys before ws are masked); a range
+  // shorter than the tiles starts at 0 and reads up to the zeroed V^T columns.
+  if (t0 + 32 * nt > lim) t0 = max(0, lim - 32 * nt);
+  t0 = __builtin_amdgcn_readfirstlane(t0);
+
+  // Keys this lane's query sees, as LDS key offsets: [vlo, vhi). Tiles inside the band that every
+  // query of the wave sees, [blo, bhi), need no mask.
+  const int vlo = max(kb0, qk - W) - cstart, vhi = min(kb1, qk + W + 1) - cstart;
+  const int blo = __builtin_amdgcn_readfirstlane(max(kb0, min(wq0 + 31, tl.q1 - 1) - W) - cstart);
+  const int bhi = __builtin_amdgcn_readfirstlane(min(kb1, wq0 + W + 1) - cstart);
+  f32x16 s[LTILES];
+  float mx = NEG_INF;
+#pragma unroll
+  for (int t = 0; t < LTILES; ++t) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[t][e] = NEG_INF;
+    if (t >= nt) continue;
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[(t0 + t * 32 + col) * LKW + kb * 16 + hl * 8]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], acc, 0, 0, 0);
+    }
+    const int tb = t0 + t * 32;  // LDS key offset of the tile
+    if (tb >= blo && tb + 32 <= bhi) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        s[t][e] = acc[e];
+        mx = fmaxf(mx, acc[e]);
+      }
+    } else {
+      const int lo = vlo - tb - hl * 4, hi = vhi - tb - hl * 4;  // bounds on (e >> 2) * 8 + (e & 3)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int off = (e >> 2) * 8 + (e & 3);
+        s[t][e] = off >= lo && off < hi ? acc[e] : NEG_INF;
+        mx = fmaxf(mx, s[t][e]);
+      }
+    }
+  }
+  // Every real query sees itself, so the row maximum is finite.
+  const float sl2 = a.scale * 1.4426950408889634f;
+  const float ms = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+  float psum = 0.0f;
+  f32x16 o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+#pragma unroll
+  for (int t = 0; t < LTILES; ++t) {
+    if (t >= nt) continue;
+    bf16x8 pf[2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
+        psum += p;
+        pf[sb][j] = __bf16(p);
+      }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int kbase = t0 + t * 32 + sb * 16 + hl * 4;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const uint16_t* vr = &sVt[(dt * 32 + col) * LVW];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
+        const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[sb], o[dt], 0, 0, 0);
+      }
+    }
+  }
+  const float lt = psum + __shfl_xor(psum, 32, 64);
+  if (!qvalid) return;
+  const float inv = 1.0f / lt;
+  uint16_t* orow = a.out + size_t(qi) * a.ldo + head * 64;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dim = dt * 32 + g * 8 + hl * 4;
+      uint2 w;
+      w.x = pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
+      w.y = pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + dim) = w;
+    }
+}
+
 }  // namespace
 
-int attn_tile_queries(bool local) { return local ? 128 : 256; }
+int attn_tile_queries(bool local) { return local ? LQ : 256; }
 
 void attn_launch(const AttnArgs& a, hipStream_t st) {
   if (a.ntiles <= 0) return;
   dim3 grid(a.ntiles, a.heads);
-  if (a.window >= 0)
+  if (a.window >= 0 && a.window <= LMAXW && !a.qkey)
+    hipLaunchKernelGGL(attn_local_kernel, grid, dim3(256), 0, st, a);  // tiles of <= LQ queries
+  else if (a.window >= 0)
     hipLaunchKernelGGL((attn_kernel<true, 4>), grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL((attn_kernel<false, 8>), grid, dim3(512), 0, st, a);

@@ -195,7 +195,8 @@ def attention_ref(q, k, v, starts, window, scale):
     return out
 
 
-@pytest.mark.parametrize("window", [-1, 64])
+# window 64 and 16 take the staged local kernel, 100 the chunked one, -1 the global one
+@pytest.mark.parametrize("window", [-1, 64, 16, 100])
 @pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048], [5, 3, 250, 1, 700, 9]])
 def test_attention_varlen(dev, window, lens):
     say(f"attention window={window} lens={lens}")
