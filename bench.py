@@ -44,6 +44,46 @@ def gemm_flops(name: str, T: int, P: int, R: int, d: int, I: int, S: int) -> flo
     return table.get(name, 0.0)
 
 
+def step_work(b, cfg: dict, S: int) -> dict:
+    """Algorithmic work of one request per kernel name, summed over its launches:
+    ("flop", FLOPs) for the MFMA kernels, ("byte", HBM bytes read + written once) for the
+    bandwidth-bound ones, ("both", (FLOPs, bytes)) for attention."""
+    d, I, nl = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    every, W = cfg.get("global_attn_every_n_layers", 3), cfg.get("local_attention", 128) // 2
+    n_glob = len([l for l in range(nl) if l % every == 0])
+    n_loc = nl - n_glob
+    lens = [int(x) for x in b.seq_lens]
+    T = sum(lens)
+    P, R = b.n * (1 + b.kmax), b.n * b.kmax
+    glob_pairs = sum(L * L for L in lens)
+    loc_pairs = sum(min(L, i + W + 1) - max(0, i - W) for L in lens for i in range(L))
+    head_pairs = glob_pairs + sum((1 + b.kmax) * L for L in lens)  # full layer, then the picked rows
+    att_bytes = 4 * 2 * T * d  # q, k, v read, out written, bf16
+    return {
+        "wqkv_rope": ("flop", nl * 2.0 * T * d * 3 * d),
+        "wo": ("flop", nl * 2.0 * T * d * d),
+        "wi_geglu": ("flop", nl * 2.0 * T * d * 2 * I),
+        "wo2": ("flop", nl * 2.0 * T * I * d),
+        "head_in_proj": ("flop", 2 * 2.0 * T * d * 3 * d),
+        "head_out_proj": ("flop", 2.0 * (T + P) * d * d),
+        "head_linear1": ("flop", 2.0 * (T + P) * d * 4 * d),
+        "head_linear2": ("flop", 2.0 * (T + P) * 4 * d * d),
+        "scorer1": ("flop", 2.0 * R * d * S),
+        "attn_global": ("both", (n_glob * 4.0 * d * glob_pairs, n_glob * att_bytes)),
+        "attn_local": ("both", (n_loc * 4.0 * d * loc_pairs, n_loc * att_bytes)),
+        "head_attn": ("both", (4.0 * d * head_pairs, 2 * att_bytes)),
+        "embed_ln": ("byte", 8.0 * T * d),
+        "attn_norm": ("byte", (nl - 1) * 6.0 * T * d),
+        "mlp_norm": ("byte", nl * 6.0 * T * d),
+        "final_norm": ("byte", 8.0 * T * d),
+        "head_norm1": ("byte", 2 * 6.0 * T * d),
+        "head_norm2": ("byte", 6.0 * (T + P) * d),
+        "scorer_norm": ("byte", 6.0 * R * d),
+        "head_pick": ("byte", 8.0 * P * d),
+        "pooled": ("byte", 8.0 * b.n * d),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,6 +184,29 @@ def main() -> int:
             tf = f / (avg * 1e-3) / 1e12
             kernels[name]["tflops"] = round(tf, 1)
             kernels[name]["mfma_util"] = round(tf / PEAK_BF16_TFLOPS, 4)
+    # Per-step rates against the roofline of each kernel's bound (launches of one name can differ
+    # in size, e.g. the head's full and pruned layers, so these use the step totals).
+    req_flop = 0.0
+    for name, (kind, amt) in step_work(b, MODERNBERT_LARGE, SCORER_WIDTH).items():
+        k = kernels.get(name)
+        flop, byts = (amt if kind == "both" else (amt, 0.0) if kind == "flop" else (0.0, amt))
+        req_flop += flop
+        if not k or k["total_ms_per_step"] <= 0:
+            continue
+        sec = k["total_ms_per_step"] * 1e-3
+        if flop:
+            k["step_tflops"] = round(flop / sec / 1e12, 1)
+            k["step_mfma_frac"] = round(flop / sec / 1e12 / PEAK_BF16_TFLOPS, 4)
+        if byts:
+            k["step_gbps"] = round(byts / sec / 1e9, 1)
+            k["step_hbm_frac"] = round(byts / sec / 1e9 / PEAK_HBM_GBS, 4)
+    request_roofline = {
+        "flop_per_request": req_flop,
+        "mfma_floor_ms": round(req_flop / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 4),
+        "frac": round(req_flop / (PEAK_BF16_TFLOPS * 1e12) * 1e3 / ms, 4),
+        "note": "all GEMM and attention FLOPs of one request at the 2.5 PFLOP/s dense bf16 peak, over the "
+                "measured ms/request",
+    }
     gemms = {k: v for k, v in kernels.items() if "tflops" in v}
     dom = max(gemms, key=lambda k: gemms[k]["total_ms_per_step"])
     dk = gemms[dom]
@@ -225,6 +288,7 @@ def main() -> int:
         "throughput": throughput,
         "gemm_mfma_util": {k: v["mfma_util"] for k, v in gemms.items()},
         "roofline": roofline,
+        "request_roofline": request_roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
