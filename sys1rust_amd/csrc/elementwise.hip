@@ -127,6 +127,68 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   }
 }
 
+// Split-K residual GEMM end + LayerNorm, one wave per row. The sum runs over the splits in
+// order from 0.0f, then the bias (or 0.0f), then onto h: the arithmetic of the GEMM's split-K
+// epilogue; the statistics and y are layernorm_kernel's on the new h. Two splits are loaded per
+// step so that each add waits on one load round, not one load.
+template <int PL>
+__global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __restrict__ ws, int splits,
+                                                             const float* __restrict__ bias, float* __restrict__ h,
+                                                             const float* __restrict__ w, float eps, int T, int d,
+                                                             uint16_t* __restrict__ y) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const size_t plane = size_t(T) * d;
+  const float* part = ws + size_t(row) * d + lane * 8;
+  float x[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) x[i] = 0.0f;
+  int s = 0;
+  for (; s + 2 <= splits; s += 2) {
+    float a[PL], b[PL];
+#pragma unroll
+    for (int c = 0; c < PL / 8; ++c) {
+      load8f(part + size_t(s) * plane + c * 512, a + c * 8);
+      load8f(part + size_t(s + 1) * plane + c * 512, b + c * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < PL; ++i) x[i] = (x[i] + a[i]) + b[i];
+  }
+  if (s < splits) {
+    float a[PL];
+#pragma unroll
+    for (int c = 0; c < PL / 8; ++c) load8f(part + size_t(s) * plane + c * 512, a + c * 8);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) x[i] += a[i];
+  }
+  float* hr = h + size_t(row) * d + lane * 8;
+  float v[PL], wv[PL];
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c) {
+    float hb[8], bb[8];
+    load8f(hr + c * 512, hb);
+    if (bias) {
+      load8f(bias + c * 512 + lane * 8, bb);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bb[e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[c * 8 + e] = hb[e] + (x[c * 8 + e] + bb[e]);
+    store8f(hr + c * 512, v + c * 8);
+    load8f(w + c * 512 + lane * 8, wv + c * 8);
+  }
+  float mean, rstd;
+  ln_stats<PL>(v, d, eps, mean, rstd);
+  float o[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) o[i] = (v[i] - mean) * rstd * wv[i] + 0.0f;
+#pragma unroll
+  for (int c = 0; c < PL / 8; ++c)
+    *reinterpret_cast<uint4*>(y + size_t(row) * d + c * 512 + lane * 8) = pack8(o + c * 8);
+}
+
 // One thread per (token, head, quarter of the 32 rotation pairs): pairs i0 .. i0 + 7 with
 // i0 = 8 * quarter, i.e. dims [i0, i0 + 8) and [i0 + 32, i0 + 40) of the head, for q, k and v.
 __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restrict__ qkv, int T, int d,
@@ -258,6 +320,23 @@ void layernorm_launch(const float* x, const int* rows, const float* w, const flo
       break;
     case 2048:
       hipLaunchKernelGGL(layernorm_kernel<32>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+  }
+}
+
+void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T,
+                            int d, uint16_t* y, hipStream_t st) {
+  if (T <= 0) return;
+  dim3 grid((T + 3) / 4);
+  switch (d) {
+    case 512:
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<8>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
+      break;
+    case 1024:
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<16>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
+      break;
+    case 2048:
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<32>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
   }
 }

@@ -571,9 +571,11 @@ const char* gemm_check(const GemmArgs& g) {
   return nullptr;
 }
 
+void gemm_launch_partials(const GemmArgs& g, hipStream_t st) { launch_e<EPI_F32>(g, st); }
+
 void gemm_launch(const GemmArgs& g, hipStream_t st) {
   if (g.splits > 1) {
-    launch_e<EPI_F32>(g, st);  // partials only: the kernel returns before its epilogue
+    gemm_launch_partials(g, st);  // partials only: the kernel returns before its epilogue
     const long long n = (long long)g.M * (g.N / 2);
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, g);
     return;

@@ -39,6 +39,9 @@ struct GemmArgs {
 // Null when the shape is supported, else a message.
 const char* gemm_check(const GemmArgs& g);
 void gemm_launch(const GemmArgs& g, hipStream_t st);
+// The first half of a split-K gemm_launch (g.splits > 1): the f32 partials into g.ws, no
+// epilogue. splitk_resid_ln_launch finishes a residual GEMM launched this way.
+void gemm_launch_partials(const GemmArgs& g, hipStream_t st);
 
 // The split-K factor gemm_launch should use for M x N x K (1: none), and the workspace it needs
 // in f32 elements.
@@ -91,6 +94,13 @@ void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, fl
 void layernorm_launch(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
                       uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
                       hipStream_t st);
+
+// The end of a split-K residual GEMM and the LayerNorm after it, one wave per row:
+// h[t] += (sum over s of ws[s, t] in split order) + bias, then y[t] = LN(h[t]) (weight w, no
+// bias) in bf16. Bit for bit the GEMM's own split-K epilogue followed by layernorm_launch.
+// ws is [splits, T, d] f32, h is [T, d] f32.
+void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T,
+                            int d, uint16_t* y, hipStream_t st);
 
 // Plain split (+ RoPE when cos/sin are given): qkv [T, 3d] bf16 -> q, k [H, T, 64] and v
 // transposed [H, 64, ldv] (ldv >= T), bf16.

@@ -58,6 +58,7 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "unpad") s.unpad = flag();
     else if (key == "fuserope") s.fuserope = flag();
     else if (key == "fusegeglu") s.fusegeglu = flag();
+    else if (key == "fuseln") s.fuseln = flag();
     else if (key == "graphs") s.graphs = flag();
     else if (key == "parallel_load") flag();  // read by the runtime (backend.rs:44-69); checked here too
     else if (key == "pad") {
@@ -287,6 +288,7 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
   if (set.fuserope) kernels += ",fuserope";
   kernels += ",band";
   if (set.fusegeglu) kernels += ",fusegeglu";
+  if (set.fuseln) kernels += ",fuseln";
   if (set.headprune) kernels += ",headprune";
 }
 
@@ -569,8 +571,8 @@ void Model::collect_stats() {
 
 namespace {
 
-void gemm(hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
-          const float* bias, int M, int N, int epi, int act = ACT_NONE) {
+GemmArgs gemm_args(float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
+                   const float* bias, int M, int N, int epi, int act = ACT_NONE) {
   GemmArgs g;
   g.splits = gemm_plan(M, N, K).splits;
   g.ws = ws;
@@ -587,7 +589,12 @@ void gemm(hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t*
   g.epi = epi;
   g.act = act;
   if (const char* e = gemm_check(g)) fail(kBackend, e);
-  gemm_launch(g, st);
+  return g;
+}
+
+void gemm(hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
+          const float* bias, int M, int N, int epi, int act = ACT_NONE) {
+  gemm_launch(gemm_args(ws, A, lda, W, K, C, ldc, bias, M, N, epi, act), st);
 }
 
 }  // namespace
@@ -602,10 +609,13 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
 
   // h = LN(tok_emb[ids]) (lib.rs:1534-1551); x = h for layer 0, which has no attn_norm.
   op("embed_ln", [&] { embed_ln_launch(tok_emb, ids, emb_norm, eps, T, d, a.h, a.x, stream); });
+  // A residual GEMM that splits K hands its partials to the kernel of the LayerNorm after it,
+  // which adds them into h and writes x = LN(h); x_ready marks an attn_norm done that way.
+  bool x_ready = false;
   for (int l = 0; l < cfg.layers; ++l) {
     const LayerWeights& L = layers[l];
     const int tw = L.local ? 1 : 0;
-    if (L.attn_norm)
+    if (L.attn_norm && !x_ready)
       op("attn_norm", [&] {
         layernorm_launch(a.h, nullptr, L.attn_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
       });
@@ -655,19 +665,34 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       at.window = L.local ? cfg.window() : -1;
       attn_launch(at, stream);
     });
-    // h = h + att . Wo^T (lib.rs:1666)
-    op("wo", [&] { gemm(stream, a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID); });
-    op("mlp_norm", [&] {
-      layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
-    });
+    x_ready = false;
+    // h = h + att . Wo^T (lib.rs:1666), x = mlp_norm(h) (lib.rs:1669)
+    const GemmArgs gwo = gemm_args(a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID);
+    if (set.fuseln && gwo.splits > 1) {
+      op("wo", [&] { gemm_launch_partials(gwo, stream); });
+      op("mlp_norm", [&] { splitk_resid_ln_launch(a.ws, gwo.splits, nullptr, a.h, L.mlp_norm, eps, T, d, a.x, stream); });
+    } else {
+      op("wo", [&] { gemm_launch(gwo, stream); });
+      op("mlp_norm", [&] {
+        layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+      });
+    }
     if (set.fusegeglu) {
       op("wi_geglu", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
     } else {
       op("wi", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
       op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream); });
     }
-    // h = h + act . Wo2^T (lib.rs:1675)
-    op("wo2", [&] { gemm(stream, a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID); });
+    // h = h + act . Wo2^T (lib.rs:1675), and the next layer's x = attn_norm(h) (lib.rs:1592-1595)
+    const GemmArgs gwo2 = gemm_args(a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID);
+    const float* next_norm = l + 1 < cfg.layers ? layers[l + 1].attn_norm : nullptr;
+    if (set.fuseln && gwo2.splits > 1 && next_norm) {
+      op("wo2", [&] { gemm_launch_partials(gwo2, stream); });
+      op("attn_norm", [&] { splitk_resid_ln_launch(a.ws, gwo2.splits, nullptr, a.h, next_norm, eps, T, d, a.x, stream); });
+      x_ready = true;
+    } else {
+      op("wo2", [&] { gemm_launch(gwo2, stream); });
+    }
   }
 }
 

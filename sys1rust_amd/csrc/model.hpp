@@ -22,6 +22,7 @@ struct Settings {
   bool unpad = true;       // accepted; the HIP path always runs the packed token layout
   bool fuserope = true;    // RoPE + split fused into the Wqkv GEMM epilogue
   bool fusegeglu = true;   // GeGLU fused into the Wi GEMM epilogue (Wi rows interleaved at load)
+  bool fuseln = true;      // a split-K Wo / Wo2 finishes in the kernel of the LayerNorm after it
   bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
   size_t pad = 1;          // padded_len multiple
   std::vector<size_t> buckets;

@@ -89,7 +89,7 @@ def test_gemm_f32_and_bf16_outputs(dev, M, N, K):
     assert bool((err <= ref.abs() * 2 ** -8 + 1e-5 * scale).all()), float(err.max())
 
 
-@pytest.mark.parametrize("M", [300, 1500])  # split-K (reduce kernel) and whole-K epilogues
+@pytest.mark.parametrize("M", [100, 300, 1500])  # split-K (M 100) and whole-K epilogues
 def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M):
     N, K = 1024, 512
     g = torch.Generator(device="cpu").manual_seed(5)
@@ -120,7 +120,24 @@ def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M):
     assert bool(((act - r).abs() <= r.abs() * 2 ** -7 + 1e-4).all()), float((act - r).abs().max())
 
 
-@pytest.mark.parametrize("M", [512, 2048])
+def test_split_k_back_to_back_shapes(dev):
+    """Split-K launches of other shapes and split counts in a row, each reusing the workspace
+    the previous one left: every result is complete and repeats bit for bit."""
+    g = torch.Generator(device="cpu").manual_seed(77)
+    cases = [(170, 1024, 2624), (170, 3072, 1024), (170, 1024, 2624), (64, 1024, 1024), (170, 1024, 2624)]
+    for M, N, K in cases:
+        say(f"split-K M={M} N={N} K={K}")
+        A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
+        W = bf16_bits(torch.randn(N, K, generator=g) * 0.02).to(dev)
+        ref = as_f32(A) @ as_f32(W).T
+        out = gemm(A, W, M, N, K, epi=3)
+        scale = float(ref.abs().max())
+        assert float((out - ref).abs().max()) <= 2e-5 * scale + 1e-6
+        again = gemm(A, W, M, N, K, epi=3)
+        assert torch.equal(out, again)  # partials summed in split order
+
+
+@pytest.mark.parametrize("M", [170, 512, 2048])  # 170: split-K, including the transposed v blocks
 @pytest.mark.parametrize("theta", [160000.0, 10000.0])
 def test_fused_wqkv_split_rope(dev, theta, M):
     """Isolated fused Wqkv GEMM + split + RoPE at M=512 (and 2048, the whole-K path), K=1024,

@@ -70,7 +70,8 @@ def test_small_encoder_matches_oracle_and_golden(small_model):
     assert prel <= HIDDEN_REL_GATE
 
 
-@pytest.mark.parametrize("settings", ["fuserope=0", "fusegeglu=0", "headprune=0", "fuserope=0,fusegeglu=0,headprune=0"])
+@pytest.mark.parametrize("settings", ["fuserope=0", "fusegeglu=0", "headprune=0", "fuseln=0",
+                                      "fuserope=0,fusegeglu=0,headprune=0,fuseln=0"])
 def test_settings_variants_agree(small_model, settings):
     cfg, agent, st, b, z = small_model
     say(f"variant {settings}")
@@ -85,6 +86,29 @@ def test_settings_variants_agree(small_model, settings):
         assert "fuserope" not in var.active_kernels()
     if "headprune=0" in settings:
         assert "headprune" not in var.active_kernels()
+    if settings == "fuseln=0":  # same arithmetic in one kernel instead of two
+        assert "fuseln" not in var.active_kernels() and "fuseln" in base.active_kernels()
+        assert np.array_equal(o1.logits, o2.logits) and np.array_equal(o1.pooled, o2.pooled)
+        assert np.array_equal(h1, h2)
+
+
+@pytest.mark.parametrize("settings", ["", "graphs=0"])
+def test_row_subsets_after_other_batches_match_oracle(small_model, settings):
+    """One model, batches of different shapes in a row: each must match the oracle on its own.
+    The arena is re-planned for each shape (split-K workspaces, graph capture per shape), and
+    what a launch reads must be its own batch's data, not what an earlier layout left there
+    (rows are independent, so any subset has known answers)."""
+    cfg, agent, st, b, z = small_model
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=settings)
+    o = O.Oracle(st, cfg, agent)
+    for rows in ([0, 1, 2], [1, 2], [0, 1, 2], [2], [0, 2], [1, 2], [1]):
+        bb = b.rows(rows)
+        out = m.forward(bb)
+        lg_ref, pl_ref = o.forward(bb)
+        check_answers(out.logits, lg_ref, bb, f"rows {rows}")
+        prel = float(np.linalg.norm(out.pooled - pl_ref) / np.linalg.norm(pl_ref))
+        say(f"rows {rows}: pooled rel {prel:.3e}")
+        assert prel <= HIDDEN_REL_GATE, (rows, prel)
 
 
 def test_graph_replays_match_eager_runs(small_model):
@@ -150,6 +174,21 @@ def test_modernbert_large_ten_questions(large):
     # other GEMM splits, so bf16 rounding differs in the last bits; compare at the answer gates.)
     alone = m.forward(sub)
     check_answers(alone.logits, lg, sub, "state512_10q rows alone")
+
+
+def test_fused_split_k_layernorm_bit_exact(large):
+    """At one short request Wo and Wo2 split K and finish inside the next LayerNorm's kernel;
+    with fuseln=0 the same sums run in the GEMM's reduce kernel and a separate LayerNorm."""
+    m, _ = large
+    st = synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
+    sep = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="fuseln=0")
+    for name in ("state128_1q", "state512_1q"):
+        b = workload(name, seed=3)
+        say(f"fuseln {name}: T={b.total_tokens()}")
+        o1, o2 = m.forward(b), sep.forward(b)
+        assert np.array_equal(o1.logits, o2.logits) and np.array_equal(o1.pooled, o2.pooled), name
+        assert np.array_equal(m.encoder_hidden(b), sep.encoder_hidden(b)), name
+    sep.close()
 
 
 def test_warmup_and_repeat_determinism(large):
