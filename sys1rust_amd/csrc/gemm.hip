@@ -433,30 +433,43 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
                      st, g);
 }
 
-// Tile configurations, chosen from the number of 128 x 128 tiles the GEMM has (the GPU holds
-// two workgroups on each of its 256 CUs):
-//   small  (one request of up to ~1000 tokens, or fewer than 200 tiles): 64 x 128 tiles in 4
-//          waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two workgroups per CU);
-//          these GEMMs stream their weights, so load depth matters more than operand reuse;
-//   mid    (fewer than 700 tiles, e.g. the 1024-wide Wo / Wo2 at a 10-question request): the same
-//          64 x 128 tiles, two stages; twice the tiles spread evenly over the CUs where 128-row
-//          tiles leave most CUs one tile and some two;
-//   large  128 x 128 tiles in 4 waves of 64 x 64, two stages (64 KiB, two per CU).
+// Tile configurations, chosen from the number of tiles the GEMM has (the GPU holds two
+// workgroups on each of its 256 CUs):
+//   small  (one request of up to ~1000 tokens, or fewer than 200 128 x 128 tiles): 64 x 128
+//          tiles in 4 waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two
+//          workgroups per CU); these GEMMs stream their weights, so load depth matters more than
+//          operand reuse;
+//   wide   (at least 400 192 x 128 tiles, e.g. Wqkv and Wi at a 10-question request): 192 x 128
+//          tiles in 4 waves of 96 x 64, two stages (80 KiB, two per CU, the whole LDS). Per
+//          k-tile a CU moves 40 KiB for 3.1 MFLOP (128 x 128: 32 KiB for 2.1 MFLOP), and each
+//          wave's 6 MFMAs per fragment pair cover the LDS reads of the next k-step;
+//   mid    (the rest, e.g. the 1024-wide Wo / Wo2 at a 10-question request): the same 64 x 128
+//          tiles as small, two stages (48 KiB, three per CU); three times the tiles of 192-row
+//          tiles, spread evenly over the CUs where 192-row tiles would leave some CUs idle.
+// (A tile count that reaches 700 128 x 128 tiles always reaches 400 192 x 128 tiles, so 128-row
+// tiles are not used.)
 constexpr int SMALL_M = 1024;
-enum TileCfg { TC_SMALL, TC_MID, TC_LARGE };
+enum TileCfg { TC_SMALL, TC_WIDE, TC_MID };
 inline TileCfg tile_cfg(int M, int N) {
   if (M <= SMALL_M) return TC_SMALL;
   const long long t128 = (long long)((M + 127) / 128) * (N / 128);
-  return t128 < 200 ? TC_SMALL : t128 < 700 ? TC_MID : TC_LARGE;
+  if (t128 < 200) return TC_SMALL;
+  const long long t192 = (long long)((M + 191) / 192) * (N / 128);
+  return t192 >= 400 ? TC_WIDE : TC_MID;
 }
-inline int tile_m_of(int M, int N) { return tile_cfg(M, N) == TC_LARGE ? 128 : 64; }
+inline int tile_m_of(int M, int N) {
+  switch (tile_cfg(M, N)) {
+    case TC_WIDE: return 192;
+    default: return 64;
+  }
+}
 
 template <int EPI>
 void launch_e(const GemmArgs& g, hipStream_t st) {
   switch (tile_cfg(g.M, g.N)) {
     case TC_SMALL: launch_t<64, 128, 64, 3, 2, 2, EPI>(g, st); break;
+    case TC_WIDE: launch_t<192, 128, 64, 2, 2, 2, EPI>(g, st); break;
     case TC_MID: launch_t<64, 128, 64, 2, 2, 2, EPI>(g, st); break;
-    case TC_LARGE: launch_t<128, 128, 64, 2, 2, 2, EPI>(g, st); break;
   }
 }
 

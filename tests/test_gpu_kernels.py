@@ -69,8 +69,10 @@ def as_f32(bits):
     return bits.contiguous().view(torch.bfloat16).float()
 
 
+# Tile configurations: small (M <= 1024 or few tiles, split-K below 96 tiles), mid (1024-wide
+# outputs), large and wide (192-row tiles; 2001 and 11372 also end on partial row tiles).
 SHAPES = [(1, 128, 64), (37, 256, 128), (170, 3072, 1024), (257, 1024, 1024), (563, 1024, 2624), (600, 5248, 1024),
-          (1000, 4096, 1024)]
+          (1000, 4096, 1024), (2001, 5248, 1024), (5686, 1024, 1024), (11372, 1024, 2624)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -89,9 +91,9 @@ def test_gemm_f32_and_bf16_outputs(dev, M, N, K):
     assert bool((err <= ref.abs() * 2 ** -8 + 1e-5 * scale).all()), float(err.max())
 
 
-@pytest.mark.parametrize("M", [100, 300, 1500])  # split-K (M 100) and whole-K epilogues
-def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M):
-    N, K = 1024, 512
+@pytest.mark.parametrize("M,N", [(100, 1024), (300, 1024), (1500, 1024), (3100, 3072)])  # split-K, small, wide
+def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M, N):
+    K = 512
     g = torch.Generator(device="cpu").manual_seed(5)
     A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
     W = bf16_bits(torch.randn(N, K, generator=g) * 0.05).to(dev)
@@ -137,7 +139,7 @@ def test_split_k_back_to_back_shapes(dev):
         assert torch.equal(out, again)  # partials summed in split order
 
 
-@pytest.mark.parametrize("M", [170, 512, 2048])  # 170: split-K, including the transposed v blocks
+@pytest.mark.parametrize("M", [170, 512, 2048, 4100])  # 170: split-K, including the transposed v blocks; 4100: wide
 @pytest.mark.parametrize("theta", [160000.0, 10000.0])
 def test_fused_wqkv_split_rope(dev, theta, M):
     """Isolated fused Wqkv GEMM + split + RoPE at M=512 (and 2048, the whole-K path), K=1024,
