@@ -23,6 +23,11 @@
 // reuses P^T straight from the S^T accumulators: within a 16-key MFMA step, operand slot
 // 8h + j stands for key 16s + 8(j / 4) + 4h + (j % 4), and the V^T operand is read from LDS with
 // the same key order (two 8-byte reads), so no shuffle of P is needed.
+//
+// Softmax weights are 2^x by the bare v_exp_f32 (__builtin_amdgcn_exp2f): it flushes results
+// below 2^-126 to 0, weights far below anything the f32 sums or the bf16 P can hold next to the
+// row maximum's 1. exp2f wraps the instruction in a denormal-range fixup of five more VALU
+// instructions per weight, and these kernels are VALU-bound.
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -200,7 +205,7 @@ void attn_kernel(AttnArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mn = fmaxf(m, mx * sl2);
       const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is exp2(-inf) = 0
-      const float alpha = exp2f(m - ms);
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);
       float psum = 0.0f;
       bf16x8 pf[2][2];
 #pragma unroll
@@ -209,14 +214,18 @@ void attn_kernel(AttnArgs a) {
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const float p = exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
             psum += p;
             pf[t][sb][j] = __bf16(p);
           }
       l = l * alpha + psum;
       m = mn;
+      // Once the running maximum settles, alpha is exactly 1 on every lane and the branch (taken
+      // by lanes, skipped by the wave when none needs it) saves the 32 multiplies.
+      if (alpha != 1.0f) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+        for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+      }
 
       // O^T += V^T . P^T over the needed tiles (MFMA k-steps of 16 keys), both 32-dim halves.
 #pragma unroll
@@ -414,7 +423,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p = exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
         psum += p;
         pf[sb][j] = __bf16(p);
       }
