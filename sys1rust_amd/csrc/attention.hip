@@ -39,6 +39,17 @@ constexpr int KC = 64;     // keys per chunk
 constexpr int LDS_W = 72;  // padded LDS row (bf16 elements)
 constexpr float NEG_INF = -__builtin_huge_valf();
 
+// The first `valid` bf16 elements of an 8-element piece, the rest zeroed: selects, no branches
+// (a per-element branch costs a divergent region per element on every staged piece).
+__device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
+  auto m = [valid](int e) { return (valid > e ? 0x0000ffffu : 0u) | (valid > e + 1 ? 0xffff0000u : 0u); };
+  v.x &= m(0);
+  v.y &= m(2);
+  v.z &= m(4);
+  v.w &= m(6);
+  return v;
+}
+
 // Three waves per SIMD for the local kernel (register budget 168), four for the global one.
 template <bool LOCAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
@@ -110,13 +121,7 @@ void attn_kernel(AttnArgs a) {
         const int dim = q >> 3, kc = (q & 7) * 8;
         uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c0 + kc);
         const int valid = kb1 - (c0 + kc);  // keys of this piece inside the range
-        if (valid < 8) {
-          uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-          v = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+        if (valid < 8) v = keep_first(v, valid);
         stage[it] = v;
       }
     }
@@ -328,13 +333,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         const int c = cstart + g8 * 8;
         uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c);
         const int valid = kb1 - c;
-        if (valid < 8) {
-          uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-          v = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+        if (valid < 8) v = keep_first(v, valid);
         st[it] = v;
       }
     }
