@@ -56,7 +56,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ?
 void attn_kernel(AttnArgs a) {
   constexpr int NT = NW * 64;
   constexpr int PIECES = 2 * KC * 8;  // 16-byte pieces per chunk: K [64][64] and V^T [64][64]
-  constexpr int PPT = PIECES / NT;    // pieces per thread
+  constexpr int PPT = (PIECES + NT - 1) / NT;  // pieces per thread (the last round may be partial)
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][KC * LDS_W];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[2][64 * LDS_W];
 
@@ -112,6 +112,7 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < PPT; ++it) {
       const int p = tid + it * NT;
+      if (PIECES % NT && p >= PIECES) break;
       if (p < KC * 8) {  // K piece: key p / 8, dims (p % 8) * 8
         const int key = p >> 3, dc = (p & 7) * 8;
         const int kg = min(c0 + key, kb1 - 1);
@@ -130,6 +131,7 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < PPT; ++it) {
       const int p = tid + it * NT;
+      if (PIECES % NT && p >= PIECES) break;
       if (p < KC * 8) {
         *reinterpret_cast<uint4*>(&sK[buf][(p >> 3) * LDS_W + (p & 7) * 8]) = stage[it];
       } else {
