@@ -283,16 +283,20 @@ void attn_kernel(AttnArgs a) {
 constexpr int LQ = 128;                 // queries per workgroup: 4 waves x 32
 constexpr int LMAXW = 64;               // largest window this kernel stages
 constexpr int LMAXK = LQ + 2 * LMAXW + 8;  // staged keys: the range plus 8-alignment slack
-constexpr int LKW = 72;                 // K row in LDS (bf16): 36 words, 16 rows per 16-byte phase on distinct banks
+// K rows in LDS are 128 bytes (64 bf16) with 16-byte chunk c of row r at slot c ^ ((r / 2) % 8):
+// the 16 rows of one 16-byte-read phase then hit 16 distinct bank groups, and each 8-row group is
+// one contiguous KiB that a single direct global -> LDS load (global_load_lds_dwordx4) fills.
+__device__ __forceinline__ int kslot(int r, int c) { return c ^ ((r >> 1) & 7); }
 // V^T row in LDS (bf16): 146 words (2 x odd), so the 32 lanes' 8-byte reads of one access hit
 // 64 distinct banks; 292 >= LMAXK rounded up to 32 keys, the furthest column a tile reads.
 constexpr int LVW = 292;
 constexpr int LTILES = (32 + 2 * LMAXW + 7 + 31) / 32;  // 32-key tiles a wave's window spans
 constexpr int LG = (LMAXK + 31) / 32 * 4;  // V^T 8-key groups per dim row staged or zeroed (36)
-constexpr int LPIECES = (LMAXK * 8 + 64 * LG + 255) / 256;  // 16-byte pieces per thread
+constexpr int LVR = 64 * LG / 256;             // rounds of V^T pieces (64 dims x LG groups)
+static_assert(64 * LG % 256 == 0, "V^T pieces fill whole rounds");
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_local_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[LMAXK * LKW];
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[LMAXK * 64];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[64 * LVW];
 
   const AttnTile tl = a.tiles[blockIdx.x];
@@ -315,41 +319,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int nk8 = (kb1 - cstart + 7) >> 3;  // 8-key groups staged (<= LMAXK / 8)
   const int lim = nk8 * 8;                  // staged keys
   const int ng = ((lim + 31) & ~31) / 8;    // V^T groups staged (< nk8) or zeroed, up to 32-key multiple
-  const int kp = nk8 * 64;                  // K pieces: 8 per key
-  const int np = kp + 64 * LG;              // + V^T slots: 64 dims x LG groups (those >= ng idle)
+  // Staging: K by direct loads (no registers); V^T through registers in a fixed number of rounds,
+  // every load issued before the first store. The V^T loads take clamped (in-range, finite)
+  // sources instead of branching; only the stores are conditional. V^T rows are 8-byte aligned
+  // (the padding that keeps the PV reads conflict-free), so each 16-byte piece is stored as two
+  // 8-byte halves.
   {
-    uint4 st[LPIECES];
-#pragma unroll
-    for (int it = 0; it < LPIECES; ++it) {
-      const int p = tid + it * 256;
-      if (p < kp) {
-        const int key = p >> 3, dc = (p & 7) * 8;
-        st[it] = *reinterpret_cast<const uint4*>(Kh + size_t(min(cstart + key, kb1 - 1)) * 64 + dc);
-      } else if (p < np) {
-        const int q = p - kp;
-        const int dim = q / LG, g8 = q - dim * LG;
-        if (g8 >= nk8) {  // past the staged keys: zero (only the groups below ng are stored)
-          st[it] = make_uint4(0, 0, 0, 0);
-          continue;
-        }
-        const int c = cstart + g8 * 8;
-        uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c);
-        const int valid = kb1 - c;
-        if (valid < 8) v = keep_first(v, valid);
-        st[it] = v;
+    // K: 8-row groups by direct loads, groups w, w + 4, ... from wave w; rows past kb1 repeat
+    // the last key (masked out of S).
+    {
+      const int r = lane >> 3, slot = lane & 7;
+      for (int gi = wave; gi < nk8; gi += 4) {
+        const int row = gi * 8 + r;
+        const uint16_t* src = Kh + size_t(min(cstart + row, kb1 - 1)) * 64 + kslot(row, slot) * 8;
+        __builtin_amdgcn_global_load_lds(src, reinterpret_cast<char*>(sK) + gi * 1024, 16, 0, 0);
       }
     }
+    uint4 vst[LVR];
 #pragma unroll
-    for (int it = 0; it < LPIECES; ++it) {
-      const int p = tid + it * 256;
-      if (p < kp) {
-        *reinterpret_cast<uint4*>(&sK[(p >> 3) * LKW + (p & 7) * 8]) = st[it];
-      } else if (p < np) {
-        const int q = p - kp;
-        const int dim = q / LG, g8 = q - dim * LG;
-        if (g8 < ng) *reinterpret_cast<uint4*>(&sVt[dim * LVW + g8 * 8]) = st[it];
+    for (int r = 0; r < LVR; ++r) {
+      const int q = tid + r * 256;  // < 64 LG
+      const int dim = q / LG, g8 = q - dim * LG;
+      const int c = cstart + min(g8, nk8 - 1) * 8;
+      uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c);
+      const int valid = g8 < nk8 ? kb1 - c : 0;  // groups past the staged keys are zero
+      if (valid < 8) v = keep_first(v, valid);
+      vst[r] = v;
+    }
+#pragma unroll
+    for (int r = 0; r < LVR; ++r) {
+      const int q = tid + r * 256;
+      const int dim = q / LG, g8 = q - dim * LG;
+      if (g8 < ng) {
+        uint2* d = reinterpret_cast<uint2*>(&sVt[dim * LVW + g8 * 8]);
+        d[0] = make_uint2(vst[r].x, vst[r].y);
+        d[1] = make_uint2(vst[r].z, vst[r].w);
       }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct K loads have landed
   }
   __syncthreads();
 
@@ -389,7 +396,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[(t0 + t * 32 + col) * LKW + kb * 16 + hl * 8]);
+      const int kr = t0 + t * 32 + col;
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[kr * 64 + kslot(kr, kb * 2 + hl) * 8]);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], acc, 0, 0, 0);
     }
     const int tb = t0 + t * 32;  // LDS key offset of the tile
