@@ -39,17 +39,6 @@ constexpr int KC = 64;     // keys per chunk
 constexpr int LDS_W = 72;  // padded LDS row (bf16 elements)
 constexpr float NEG_INF = -__builtin_huge_valf();
 
-// The first `valid` bf16 elements of an 8-element piece, the rest zeroed: selects, no branches
-// (a per-element branch costs a divergent region per element on every staged piece).
-__device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
-  auto m = [valid](int e) { return (valid > e ? 0x0000ffffu : 0u) | (valid > e + 1 ? 0xffff0000u : 0u); };
-  v.x &= m(0);
-  v.y &= m(2);
-  v.z &= m(4);
-  v.w &= m(6);
-  return v;
-}
-
 // Three waves per SIMD for the local kernel (register budget 168), four for the global one.
 template <bool LOCAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
@@ -287,17 +276,17 @@ constexpr int LMAXK = LQ + 2 * LMAXW + 8;  // staged keys: the range plus 8-alig
 // the 16 rows of one 16-byte-read phase then hit 16 distinct bank groups, and each 8-row group is
 // one contiguous KiB that a single direct global -> LDS load (global_load_lds_dwordx4) fills.
 __device__ __forceinline__ int kslot(int r, int c) { return c ^ ((r >> 1) & 7); }
-// V^T row in LDS (bf16): 146 words (2 x odd), so the 32 lanes' 8-byte reads of one access hit
-// 64 distinct banks; 292 >= LMAXK rounded up to 32 keys, the furthest column a tile reads.
-constexpr int LVW = 292;
+// V^T rows in LDS: LVC 16-byte chunks of 8 keys (LVC odd, so the 16 rows of one 16-lane read
+// phase start in 16 distinct bank groups); LVC x 8 >= LMAXK rounded up to 32 keys, the furthest
+// column a tile reads. Each KiB of the 64 rows is filled by one direct global -> LDS load.
+constexpr int LVC = 37;
+constexpr int LVW = LVC * 8;
 constexpr int LTILES = (32 + 2 * LMAXW + 7 + 31) / 32;  // 32-key tiles a wave's window spans
-constexpr int LG = (LMAXK + 31) / 32 * 4;  // V^T 8-key groups per dim row staged or zeroed (36)
-constexpr int LVR = 64 * LG / 256;             // rounds of V^T pieces (64 dims x LG groups)
-static_assert(64 * LG % 256 == 0, "V^T pieces fill whole rounds");
+static_assert(LVC % 2 == 1 && LVC * 8 >= (LMAXK + 31) / 32 * 32 && 64 * LVC % 64 == 0, "V^T layout");
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_local_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t sK[LMAXK * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[64 * LVW];
+  __shared__ __attribute__((aligned(1024))) uint16_t sVt[64 * LVW];
 
   const AttnTile tl = a.tiles[blockIdx.x];
   const int head = blockIdx.y;
@@ -312,21 +301,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.Tk * 64;
   const uint16_t* __restrict__ Vt = a.v + size_t(head) * 64 * a.ldv;
 
-  // The workgroup's keys [kb0, kb1), staged from the 8-aligned cstart (keys below kb0 are masked
-  // out of S; V entries from kb1 on are zeroed, since the v buffer's slack is not initialised).
+  // The workgroup's keys [kb0, kb1), staged from the 8-aligned cstart (keys outside them are
+  // masked out of S, so their weights are exactly 0 and their V entries only need be finite).
   const int kb0 = max(tl.k0, tl.q0 - W), kb1 = min(tl.k1, tl.q1 + W);
   const int cstart = kb0 & ~7;
   const int nk8 = (kb1 - cstart + 7) >> 3;  // 8-key groups staged (<= LMAXK / 8)
   const int lim = nk8 * 8;                  // staged keys
-  const int ng = ((lim + 31) & ~31) / 8;    // V^T groups staged (< nk8) or zeroed, up to 32-key multiple
-  // Staging: K by direct loads (no registers); V^T through registers in a fixed number of rounds,
-  // every load issued before the first store. The V^T loads take clamped (in-range, finite)
-  // sources instead of branching; only the stores are conditional. V^T rows are 8-byte aligned
-  // (the padding that keeps the PV reads conflict-free), so each 16-byte piece is stored as two
-  // 8-byte halves.
+  // Staging by direct global -> LDS loads only (no registers, no per-piece branches).
   {
-    // K: 8-row groups by direct loads, groups w, w + 4, ... from wave w; rows past kb1 repeat
-    // the last key (masked out of S).
+    // K: 8-row groups, groups w, w + 4, ... from wave w; rows past kb1 repeat the last key
+    // (masked out of S).
     {
       const int r = lane >> 3, slot = lane & 7;
       for (int gi = wave; gi < nk8; gi += 4) {
@@ -335,28 +319,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         __builtin_amdgcn_global_load_lds(src, reinterpret_cast<char*>(sK) + gi * 1024, 16, 0, 0);
       }
     }
-    uint4 vst[LVR];
-#pragma unroll
-    for (int r = 0; r < LVR; ++r) {
-      const int q = tid + r * 256;  // < 64 LG
-      const int dim = q / LG, g8 = q - dim * LG;
-      const int c = cstart + min(g8, nk8 - 1) * 8;
-      uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c);
-      const int valid = g8 < nk8 ? kb1 - c : 0;  // groups past the staged keys are zero
-      if (valid < 8) v = keep_first(v, valid);
-      vst[r] = v;
-    }
-#pragma unroll
-    for (int r = 0; r < LVR; ++r) {
-      const int q = tid + r * 256;
-      const int dim = q / LG, g8 = q - dim * LG;
-      if (g8 < ng) {
-        uint2* d = reinterpret_cast<uint2*>(&sVt[dim * LVW + g8 * 8]);
-        d[0] = make_uint2(vst[r].x, vst[r].y);
-        d[1] = make_uint2(vst[r].z, vst[r].w);
+    // V^T: chunk S of the 64 x LVC chunks is row S / LVC, keys cstart + 8 (S % LVC) .. + 7.
+    // Chunks from kb1 on load the chunk holding key kb1 - 1 instead: finite values that meet
+    // weights of 0. The chunk holding kb1 - 1 may read up to 7 keys past kb1, which are the next
+    // sequence's or the zeros every v writer leaves up to the next multiple of 8 tokens.
+    {
+      const int last = cstart + (((kb1 - 1) - cstart) & ~7);
+      for (int i = wave; i < LVC; i += 4) {
+        const int S = i * 64 + lane;
+        const int dim = S / LVC, c = S - dim * LVC;
+        const int key = min(cstart + 8 * c, last);
+        __builtin_amdgcn_global_load_lds(Vt + size_t(dim) * a.ldv + key, reinterpret_cast<char*>(sVt) + i * 1024, 16, 0,
+                                         0);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct K loads have landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's direct loads have landed
   }
   __syncthreads();
 

@@ -39,6 +39,16 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
 }
 
+// The first `valid` (0..8) bf16 elements of an 8-element piece, the rest zeroed, by selects.
+__device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
+  auto m = [valid](int e) { return (valid > e ? 0x0000ffffu : 0u) | (valid > e + 1 ? 0xffff0000u : 0u); };
+  v.x &= m(0);
+  v.y &= m(2);
+  v.z &= m(4);
+  v.w &= m(6);
+  return v;
+}
+
 // Sum / max over the 64 lanes of a wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

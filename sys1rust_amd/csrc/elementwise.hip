@@ -250,6 +250,13 @@ __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restr
     vt[size_t(32 + 2 * j) * ldv] = uint16_t(wb[j]);
     vt[size_t(33 + 2 * j) * ldv] = uint16_t(wb[j] >> 16);
   }
+  if (t == T - 1)  // zeros up to the next multiple of 8 tokens, as the fused path writes them
+    for (int c = 1; t + c < (T + 7) / 8 * 8; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        vt[size_t(j) * ldv + c] = 0;
+        vt[size_t(32 + j) * ldv + c] = 0;
+      }
 }
 
 __global__ __launch_bounds__(256) void geglu_kernel(const uint16_t* __restrict__ wi, int T, int I,

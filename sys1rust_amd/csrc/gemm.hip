@@ -218,12 +218,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
         const int cg = half * HC + c;  // column within the tile
         const uint4 v = *reinterpret_cast<const uint4*>(stg + c * PV + k8 * 16);
         uint16_t* dst = g.rope_v + (size_t(head0 + cg / 64) * 64 + cg % 64) * g.rope_ldv + tok;
-        if (tok + 8 <= g.M) {
-          *reinterpret_cast<uint4*>(dst) = v;
-        } else {
-          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-          for (int e = 0; e < g.M - tok; ++e) dst[e] = uint16_t(w[e >> 1] >> (16 * (e & 1)));
-        }
+        // The row's last, partial 8-token group is written whole, zeros past M (ldv >= M
+        // rounded up to 8): readers may then load V^T in 8-byte pieces without masking them.
+        *reinterpret_cast<uint4*>(dst) = tok + 8 <= g.M ? v : keep_first(v, g.M - tok);
       }
     }
     return;
@@ -512,6 +509,11 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
       uint16_t* o = g.rope_v + (size_t(head) * 64 + i) * g.rope_ldv + row;
       o[0] = f2bf(x1);
       o[size_t(32) * g.rope_ldv] = f2bf(x2);
+      if (row == g.M - 1)  // zeros up to the next multiple of 8 tokens, as the GEMM's own epilogue
+        for (int t = 1; row + t < (g.M + 7) / 8 * 8; ++t) {
+          o[t] = 0;
+          o[size_t(32) * g.rope_ldv + t] = 0;
+        }
       return;
     }
     uint16_t* o = (part == 0 ? g.rope_q : g.rope_k) + (size_t(head) * g.rope_T + row) * 64;

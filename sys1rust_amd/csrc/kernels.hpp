@@ -52,7 +52,8 @@ struct GemmPlan {
 GemmPlan gemm_plan(int M, int N, int K);
 
 // The row stride of a transposed v buffer for T tokens: T rounded up to 8 (16-byte rows) plus
-// 64 columns of slack, so a 64-key chunk read never leaves the row.
+// 64 columns of slack, so a 64-key chunk read never leaves the row. Every writer of v stores
+// zeros in columns [T, T rounded up to 8); the rest of the slack is never written.
 inline int vt_ld(int T) { return (T + 7) / 8 * 8 + 64; }
 
 // Attention over packed variable-length rows. q, k are [H, Tq or Tk, 64] bf16 (head-major) and v

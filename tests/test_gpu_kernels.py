@@ -153,9 +153,11 @@ def test_fused_wqkv_split_rope(dev, theta, M):
     L = _lib()
     ldv = L.vt_ld(M)
     q, k = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(2))
-    vt = torch.zeros(16, 64, ldv, dtype=torch.int16, device=dev)
+    vt = torch.full((16, 64, ldv), -1, dtype=torch.int16, device=dev)
     L.check(L.lib().s1k_qkv_rope(ptr(A), ptr(W), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(vt), ldv, stream()))
     torch.cuda.synchronize()
+    m8 = (M + 7) // 8 * 8  # v columns [M, m8) are written as zeros, the rest of the slack is not written
+    assert bool((vt[:, :, M:m8] == 0).all()) and bool((vt[:, :, m8:] == -1).all())
     v = vt[:, :, :M].transpose(1, 2)  # v is written transposed, [H, 64, ldv]
     qkv = (as_f32(A) @ as_f32(W).T).cpu().numpy()
     cos, sin = O.rope_tables(theta, M, 64)
@@ -179,9 +181,11 @@ def test_split_rope_pass(dev, theta):
     L = _lib()
     ldv = L.vt_ld(M)
     q, k = (torch.zeros(16, M, 64, dtype=torch.int16, device=dev) for _ in range(2))
-    vt = torch.zeros(16, 64, ldv, dtype=torch.int16, device=dev)
+    vt = torch.full((16, 64, ldv), -1, dtype=torch.int16, device=dev)
     L.check(L.lib().s1k_split_rope(ptr(qkv), M, d, ptr(pos), theta, ptr(q), ptr(k), ptr(vt), ldv, stream()))
     torch.cuda.synchronize()
+    m8 = (M + 7) // 8 * 8  # v columns [M, m8) are written as zeros, the rest of the slack is not written
+    assert bool((vt[:, :, M:m8] == 0).all()) and bool((vt[:, :, m8:] == -1).all())
     v = vt[:, :, :M].transpose(1, 2)
     x = as_f32(qkv).cpu().numpy()
     p = pos.cpu().numpy()
@@ -227,9 +231,11 @@ def test_attention_varlen(dev, window, lens):
     qb, kb, vb = (bf16_bits(x).to(dev) for x in (q, k, v))
     L = _lib()
     ldv = L.vt_ld(T)
-    # v transposed, [H, 64, ldv]; the slack past T holds NaN bits, which must never reach the output
+    # v transposed, [H, 64, ldv]: columns [T, T rounded up to 8) hold zeros, as every v writer
+    # leaves them; the slack past that holds NaN bits, which must never reach the output
     vt = torch.full((H, 64, ldv), -1, dtype=torch.int16, device=dev)
     vt[:, :, :T] = vb.transpose(1, 2)
+    vt[:, :, T:(T + 7) // 8 * 8] = 0
     out = torch.zeros(T, H * 64, dtype=torch.int16, device=dev)
     st = np.ascontiguousarray(starts)
     L.check(L.lib().s1k_attention(ptr(qb), ptr(kb), ptr(vt), ldv, T, H, st.ctypes.data_as(L.i32p), len(lens),
