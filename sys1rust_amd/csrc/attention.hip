@@ -22,7 +22,7 @@
 //   O^T[dim, q] += V^T . P^T
 // reuses P^T straight from the S^T accumulators: within a 16-key MFMA step, operand slot
 // 8h + j stands for key 16s + 8(j / 4) + 4h + (j % 4), and the V^T operand is read from LDS with
-// the same key order (two 8-byte reads), so no shuffle of P is needed.
+// the same key order, so no shuffle of P is needed.
 //
 // Softmax weights are 2^x by the bare v_exp_f32 (__builtin_amdgcn_exp2f): it flushes results
 // below 2^-126 to 0, weights far below anything the f32 sums or the bf16 P can hold next to the
@@ -35,19 +35,23 @@ namespace s1 {
 
 namespace {
 
-constexpr int KC = 64;     // keys per chunk
-constexpr int LDS_W = 72;  // padded LDS row (bf16 elements)
+constexpr int KC = 64;  // keys per chunk
 constexpr float NEG_INF = -__builtin_huge_valf();
+
+// LDS rows of 128 bytes (64 bf16: a K row, or 64 keys of a V^T row) hold 16-byte chunk c of row
+// r at slot c ^ ((r / 2) % 8): the 16 rows of one 16-lane read phase then start in 16 distinct
+// bank groups, and each 8-row group is one contiguous KiB that a single direct global -> LDS
+// load (global_load_lds_dwordx4) fills.
+__device__ __forceinline__ int kslot(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 // Three waves per SIMD for the local kernel (register budget 168), four for the global one.
 template <bool LOCAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
 void attn_kernel(AttnArgs a) {
-  constexpr int NT = NW * 64;
-  constexpr int PIECES = 2 * KC * 8;  // 16-byte pieces per chunk: K [64][64] and V^T [64][64]
-  constexpr int PPT = (PIECES + NT - 1) / NT;  // pieces per thread (the last round may be partial)
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KC * LDS_W];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][64 * LDS_W];
+  // K and V^T double buffers, [K0 | K1 | V0 | V1], 8 KiB each.
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[4 * KC * 64];
+  auto sK = [&](int buf) { return smem + buf * KC * 64; };
+  auto sVt = [&](int buf) { return smem + (2 + buf) * KC * 64; };
 
   const AttnTile tl = a.tiles[blockIdx.x];
   const int head = blockIdx.y;
@@ -96,39 +100,46 @@ void attn_kernel(AttnArgs a) {
   for (int kb = 0; kb < 4; ++kb)
     qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
 
-  uint4 stage[PPT];
-  auto gload = [&](int c0) {
+  // A chunk's K goes global -> LDS by direct loads: 8 groups of 8 rows, one KiB each, spread
+  // over the waves; rows past kb1 repeat the last key. V^T goes through registers (one 16-byte
+  // piece of 8 keys per thread and wave of 64 threads per KiB): loaded with the K loads, stored
+  // after the chunk's math. (Direct loads for V^T too make the compiler wait for all of them
+  // before the chunk's first V^T read.) V^T pieces from kb1 on load the piece holding key
+  // kb1 - 1 (finite values that meet weights of 0); that piece may read up to 7 keys past kb1:
+  // the next sequence's, or the zeros every v writer leaves up to the next multiple of 8 tokens.
+  const int vlast = cstart + (((kb1 - 1) - cstart) & ~7);
+  constexpr int VPT = 64 * 8 / (NW * 64);  // V^T pieces per thread
+  static_assert(VPT * NW * 64 == 64 * 8, "V^T pieces split evenly over the threads");
+  uint4 vreg[VPT];
+  auto stage = [&](int c0, int buf) {
+    const int r8 = lane >> 3, slot = lane & 7;
+    for (int gi = wave; gi < 8; gi += NW) {
+      const int row = gi * 8 + r8;
+      const uint16_t* src = Kh + size_t(min(c0 + row, kb1 - 1)) * 64 + kslot(row, slot) * 8;
+      __builtin_amdgcn_global_load_lds(src, reinterpret_cast<char*>(sK(buf)) + gi * 1024, 16, 0, 0);
+    }
 #pragma unroll
-    for (int it = 0; it < PPT; ++it) {
-      const int p = tid + it * NT;
-      if (PIECES % NT && p >= PIECES) break;
-      if (p < KC * 8) {  // K piece: key p / 8, dims (p % 8) * 8
-        const int key = p >> 3, dc = (p & 7) * 8;
-        const int kg = min(c0 + key, kb1 - 1);
-        stage[it] = *reinterpret_cast<const uint4*>(Kh + size_t(kg) * 64 + dc);
-      } else {  // V^T piece: dim q / 8, keys (q % 8) * 8
-        const int q = p - KC * 8;
-        const int dim = q >> 3, kc = (q & 7) * 8;
-        uint4 v = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + c0 + kc);
-        const int valid = kb1 - (c0 + kc);  // keys of this piece inside the range
-        if (valid < 8) v = keep_first(v, valid);
-        stage[it] = v;
-      }
+    for (int it = 0; it < VPT; ++it) {
+      const int p = tid + it * NW * 64;
+      const int dim = p >> 3, c = p & 7;
+      vreg[it] = *reinterpret_cast<const uint4*>(Vt + size_t(dim) * a.ldv + min(c0 + c * 8, vlast));
     }
   };
-  auto sstore = [&](int buf) {
+  // V^T rows hold each 16-key block's keys in the PV operand order: key 16s + 8a + 4h + r at
+  // position 16s + 8h + 4a + r, so a lane's 8 operand keys (4h .. 4h + 3 and 8 + 4h .. 8 + 4h + 3
+  // of the block) are one 16-byte chunk (2s + h), read with one access. The 16-byte chunks are
+  // then placed by kslot like K's.
+  auto vstore = [&](int buf) {
 #pragma unroll
-    for (int it = 0; it < PPT; ++it) {
-      const int p = tid + it * NT;
-      if (PIECES % NT && p >= PIECES) break;
-      if (p < KC * 8) {
-        *reinterpret_cast<uint4*>(&sK[buf][(p >> 3) * LDS_W + (p & 7) * 8]) = stage[it];
-      } else {
-        const int q = p - KC * 8;
-        *reinterpret_cast<uint4*>(&sVt[buf][(q >> 3) * LDS_W + (q & 7) * 8]) = stage[it];
-      }
+    for (int it = 0; it < VPT; ++it) {
+      const int p = tid + it * NW * 64;
+      const int dim = p >> 3, c = p & 7;  // keys 8c .. 8c + 7 = 16 (c / 2) + 8 (c % 2) + 0 .. 7
+      uint16_t* row = sVt(buf) + dim * 64 + (c & 1) * 4;
+      *reinterpret_cast<uint2*>(row + kslot(dim, c & ~1) * 8) = make_uint2(vreg[it].x, vreg[it].y);
+      *reinterpret_cast<uint2*>(row + kslot(dim, c | 1) * 8) = make_uint2(vreg[it].z, vreg[it].w);
     }
   };
+  auto landed = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };  // this wave's direct loads
 
   const float sl2 = a.scale * 1.4426950408889634f;  // fold log2(e): exp(x) = exp2(x log2 e)
   float m = NEG_INF, l = 0.0f;
@@ -141,19 +152,21 @@ void attn_kernel(AttnArgs a) {
   // registers for three waves per SIMD.
   constexpr bool DB = !LOCAL;
   if constexpr (DB) {
-    gload(cstart);
-    sstore(0);
+    stage(cstart, 0);
+    vstore(0);
+    landed();
     __syncthreads();
   }
   int buf = 0;
   for (int c0 = cstart; c0 < kb1; c0 += KC, buf ^= (DB ? 1 : 0)) {
     const bool more = DB && c0 + KC < kb1;
     if constexpr (DB) {
-      if (more) gload(c0 + KC);
+      if (more) stage(c0 + KC, buf ^ 1);  // the other buffer was last read before the previous barrier
     } else {
       if (c0 != cstart) __syncthreads();  // every wave is done with the previous chunk
-      gload(c0);
-      sstore(0);
+      stage(c0, 0);
+      vstore(0);
+      landed();
       __syncthreads();
     }
     bool work = wave_active;
@@ -182,7 +195,8 @@ void attn_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][(t * 32 + col) * LDS_W + kb * 16 + hl * 8]);
+          const int kr = t * 32 + col;
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK(buf) + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
           s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
         }
         if (edge) {
@@ -229,21 +243,20 @@ void attn_kernel(AttnArgs a) {
         if (!need[t]) continue;
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
-          const int kbase = t * 32 + sb * 16 + hl * 4;
 #pragma unroll
           for (int dt = 0; dt < 2; ++dt) {
-            const uint16_t* vr = &sVt[buf][(dt * 32 + col) * LDS_W];
-            const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
-            const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
-            const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
+            const int dr = dt * 32 + col;
+            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sVt(buf) + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
             o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
           }
         }
       }
     }
     if constexpr (DB) {
-      if (more) sstore(buf ^ 1);  // the other buffer was last read before the previous barrier
+      if (more) {
+        vstore(buf ^ 1);  // the other buffer was last read before the previous barrier
+        landed();
+      }
       __syncthreads();
     }
   }
@@ -272,10 +285,6 @@ void attn_kernel(AttnArgs a) {
 constexpr int LQ = 128;                 // queries per workgroup: 4 waves x 32
 constexpr int LMAXW = 64;               // largest window this kernel stages
 constexpr int LMAXK = LQ + 2 * LMAXW + 8;  // staged keys: the range plus 8-alignment slack
-// K rows in LDS are 128 bytes (64 bf16) with 16-byte chunk c of row r at slot c ^ ((r / 2) % 8):
-// the 16 rows of one 16-byte-read phase then hit 16 distinct bank groups, and each 8-row group is
-// one contiguous KiB that a single direct global -> LDS load (global_load_lds_dwordx4) fills.
-__device__ __forceinline__ int kslot(int r, int c) { return c ^ ((r >> 1) & 7); }
 // V^T rows in LDS: LVC 16-byte chunks of 8 keys (LVC odd, so the 16 rows of one 16-lane read
 // phase start in 16 distinct bank groups); LVC x 8 >= LMAXK rounded up to 32 keys, the furthest
 // column a tile reads. Each KiB of the 64 rows is filled by one direct global -> LDS load.
