@@ -129,9 +129,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 
 // Split-K residual GEMM end + LayerNorm, one wave per row. The sum runs over the splits in
 // order from 0.0f, then the bias (or 0.0f), then onto h: the arithmetic of the GEMM's split-K
-// epilogue; the statistics and y are layernorm_kernel's on the new h. Two splits are loaded per
-// step so that each add waits on one load round, not one load.
-template <int PL>
+// epilogue; the statistics and y are layernorm_kernel's on the new h. The splits are loaded SG
+// at a time, all in flight together, so the row waits on ceil(splits / SG) load rounds.
+template <int PL, int SG = 32 / PL * 4>
 __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __restrict__ ws, int splits,
                                                              const float* __restrict__ bias, float* __restrict__ h,
                                                              const float* __restrict__ w, float eps, int T, int d,
@@ -144,23 +144,18 @@ __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __res
   float x[PL];
 #pragma unroll
   for (int i = 0; i < PL; ++i) x[i] = 0.0f;
-  int s = 0;
-  for (; s + 2 <= splits; s += 2) {
-    float a[PL], b[PL];
+  for (int s = 0; s < splits; s += SG) {
+    float a[SG][PL];
 #pragma unroll
-    for (int c = 0; c < PL / 8; ++c) {
-      load8f(part + size_t(s) * plane + c * 512, a + c * 8);
-      load8f(part + size_t(s + 1) * plane + c * 512, b + c * 8);
-    }
+    for (int u = 0; u < SG; ++u)
 #pragma unroll
-    for (int i = 0; i < PL; ++i) x[i] = (x[i] + a[i]) + b[i];
-  }
-  if (s < splits) {
-    float a[PL];
+      for (int c = 0; c < PL / 8; ++c) load8f(part + size_t(min(s + u, splits - 1)) * plane + c * 512, a[u] + c * 8);
 #pragma unroll
-    for (int c = 0; c < PL / 8; ++c) load8f(part + size_t(s) * plane + c * 512, a + c * 8);
+    for (int u = 0; u < SG; ++u)
+      if (s + u < splits) {
 #pragma unroll
-    for (int i = 0; i < PL; ++i) x[i] += a[i];
+        for (int i = 0; i < PL; ++i) x[i] += a[u][i];
+      }
   }
   float* hr = h + size_t(row) * d + lane * 8;
   float v[PL], wv[PL];

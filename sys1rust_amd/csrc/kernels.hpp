@@ -44,12 +44,14 @@ void gemm_launch(const GemmArgs& g, hipStream_t st);
 void gemm_launch_partials(const GemmArgs& g, hipStream_t st);
 
 // The split-K factor gemm_launch should use for M x N x K (1: none), and the workspace it needs
-// in f32 elements.
+// in f32 elements. reduce_folded: the caller finishes a split in a kernel it runs anyway
+// (splitk_resid_ln_launch), so splitting pays at more tile counts. A folded plan splits wherever
+// an unfolded one does, with the same factor.
 struct GemmPlan {
   int splits;
   size_t ws_floats;
 };
-GemmPlan gemm_plan(int M, int N, int K);
+GemmPlan gemm_plan(int M, int N, int K, bool reduce_folded = false);
 
 // The row stride of a transposed v buffer for T tokens: T rounded up to 8 (16-byte rows) plus
 // 64 columns of slack, so a 64-key chunk read never leaves the row. Every writer of v stores

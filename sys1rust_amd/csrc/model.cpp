@@ -480,7 +480,7 @@ Model::Acts Model::arena(const Plan& p) {
   const int shapes[][3] = {{Ti, 3 * di, di}, {Ti, di, di}, {Ti, 2 * Ii, di}, {Ti, di, Ii}, {Ti, 4 * di, di},
                            {Ti, di, 4 * di}, {Pi, di, di}, {Pi, 4 * di, di}, {Pi, di, 4 * di}, {Ri, Si, di}};
   for (const auto& sh : shapes)
-    if (sh[0] > 0) wsf = std::max(wsf, gemm_plan(sh[0], sh[1], sh[2]).ws_floats);
+    if (sh[0] > 0) wsf = std::max(wsf, gemm_plan(sh[0], sh[1], sh[2], true).ws_floats);  // >= the unfolded plan's
   const size_t vbytes = d * size_t(vt_ld(int(T))) * 2;  // v transposed, [H, 64, ldv]
   size_t sizes[] = {T * d * 4, T * d * 2, T * d * 2, T * d * 2, vbytes, T * 3 * d * 2, T * d * 2,
                     T * midw * 2, T * I * 2, T * d * 4, T * d * 4, P * d * 4, P * d * 2, P * d * 2,
@@ -572,9 +572,9 @@ void Model::collect_stats() {
 namespace {
 
 GemmArgs gemm_args(float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
-                   const float* bias, int M, int N, int epi, int act = ACT_NONE) {
+                   const float* bias, int M, int N, int epi, int act = ACT_NONE, bool reduce_folded = false) {
   GemmArgs g;
-  g.splits = gemm_plan(M, N, K).splits;
+  g.splits = gemm_plan(M, N, K, reduce_folded).splits;
   g.ws = ws;
   g.A = A;
   g.W = W;
@@ -667,7 +667,9 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
     });
     x_ready = false;
     // h = h + att . Wo^T (lib.rs:1666), x = mlp_norm(h) (lib.rs:1669)
-    const GemmArgs gwo = gemm_args(a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID);
+    // Wo and Wo2 plan their split as finished by the LayerNorm after them (structurally, so the
+    // fuseln=0 path splits the same way and stays bit-identical).
+    const GemmArgs gwo = gemm_args(a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, true);
     if (set.fuseln && gwo.splits > 1) {
       op("wo", [&] { gemm_launch_partials(gwo, stream); });
       op("mlp_norm", [&] { splitk_resid_ln_launch(a.ws, gwo.splits, nullptr, a.h, L.mlp_norm, eps, T, d, a.x, stream); });
@@ -684,8 +686,8 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream); });
     }
     // h = h + act . Wo2^T (lib.rs:1675), and the next layer's x = attn_norm(h) (lib.rs:1592-1595)
-    const GemmArgs gwo2 = gemm_args(a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID);
     const float* next_norm = l + 1 < cfg.layers ? layers[l + 1].attn_norm : nullptr;
+    const GemmArgs gwo2 = gemm_args(a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, next_norm != nullptr);
     if (set.fuseln && gwo2.splits > 1 && next_norm) {
       op("wo2", [&] { gemm_launch_partials(gwo2, stream); });
       op("attn_norm", [&] { splitk_resid_ln_launch(a.ws, gwo2.splits, nullptr, a.h, next_norm, eps, T, d, a.x, stream); });
