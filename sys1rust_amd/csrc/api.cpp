@@ -374,11 +374,12 @@ int s1k_attention(const void* q, const void* k, const void* v, int v_ld, int T, 
     if (!seq_starts || nseq < 1) s1::fail(s1::kConfig, "s1k_attention: need seq_starts");
     if (seq_starts[0] != 0 || seq_starts[nseq] != T) s1::fail(s1::kConfig, "s1k_attention: seq_starts must run 0..T");
     if (v_ld < s1::vt_ld(T)) s1::fail(s1::kConfig, "s1k_attention: v_ld must be at least T rounded up to 8, plus 64");
-    const int qb = s1::attn_tile_queries(window >= 0);
+    for (int r = 0; r < nseq; ++r)
+      if (seq_starts[r + 1] <= seq_starts[r]) s1::fail(s1::kConfig, "s1k_attention: empty or decreasing sequence");
+    const int qb = window >= 0 ? s1::attn_tile_queries(true) : s1::attn_global_tile(seq_starts, nseq, H);
     std::vector<int> tiles;
     for (int r = 0; r < nseq; ++r) {
       const int rs = seq_starts[r], re = seq_starts[r + 1];
-      if (re <= rs) s1::fail(s1::kConfig, "s1k_attention: empty or decreasing sequence");
       for (int q0 = rs; q0 < re; q0 += qb) {
         tiles.push_back(q0);
         tiles.push_back(std::min(q0 + qb, re));
@@ -403,6 +404,7 @@ int s1k_attention(const void* q, const void* k, const void* v, int v_ld, int T, 
     a.ldo = H * 64;
     a.scale = scale;
     a.window = window;
+    a.tile_q = qb;
     s1::attn_launch(a, st);
     hipError_t e = hipGetLastError();
     hip_ok(hipStreamSynchronize(st), "s1k_attention");

@@ -456,6 +456,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
 int attn_tile_queries(bool local) { return local ? LQ : 256; }
 
+// 256-query tiles (8 waves, every K/V chunk shared by 256 queries) while they give at least one
+// workgroup per CU; a short request instead takes 128 or 64 (fewer queries per K/V chunk, but
+// more of the 256 CUs at work): the first that gives 128 workgroups, else 64.
+int attn_global_tile(const int* row_start, int n, int heads) {
+  auto count = [&](int qb) {
+    long long c = 0;
+    for (int r = 0; r < n; ++r) c += (row_start[r + 1] - row_start[r] + qb - 1) / qb;
+    return c * heads;
+  };
+  if (count(256) >= 256) return 256;
+  return count(128) >= 128 ? 128 : 64;
+}
+
 void attn_launch(const AttnArgs& a, hipStream_t st) {
   if (a.ntiles <= 0) return;
   dim3 grid(a.ntiles, a.heads);
@@ -463,8 +476,12 @@ void attn_launch(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(attn_local_kernel, grid, dim3(256), 0, st, a);  // tiles of <= LQ queries
   else if (a.window >= 0)
     hipLaunchKernelGGL((attn_kernel<true, 4>), grid, dim3(256), 0, st, a);
-  else
+  else if (a.tile_q == 256)
     hipLaunchKernelGGL((attn_kernel<false, 8>), grid, dim3(512), 0, st, a);
+  else if (a.tile_q == 128)
+    hipLaunchKernelGGL((attn_kernel<false, 4>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(128), 0, st, a);
 }
 
 }  // namespace s1

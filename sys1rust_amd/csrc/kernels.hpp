@@ -82,10 +82,13 @@ struct AttnArgs {
   int ldo = 0;
   float scale = 0.125f;
   int window = -1;  // < 0: global attention; else keys with |i - j| <= window
+  int tile_q = 256;  // global attention: the tiles' query count, 256, 128 or 64 (8, 4 or 2 waves)
 };
 void attn_launch(const AttnArgs& a, hipStream_t st);
-// Queries per work tile the attention kernel takes (global layers use larger workgroups).
+// Queries per work tile the attention kernel takes: 128 on local layers; on global layers the
+// largest of 256, 128 and 64 that still gives the GPU enough workgroups, given the rows' lengths.
 int attn_tile_queries(bool local);
+int attn_global_tile(const int* row_start, int n, int heads);
 
 // h[t] = LN(tok_emb[ids[t]]) (no bias), written as f32 and as bf16.
 void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,

@@ -400,8 +400,9 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
     while (m.size() % 4) m.push_back(0);
   };
   pad4();
-  // Attention work tiles: query blocks of one row, 256 queries for global layers (one
-  // workgroup of 8 waves), 128 for local ones (4 waves; their keys are only the window).
+  // Attention work tiles: query blocks of one row; for global layers 256 queries (one workgroup
+  // of 8 waves), or 128 / 64 for a short batch (attn_global_tile); 128 for local ones (4 waves;
+  // their keys are only the window).
   auto tiles = [&](int qb, int& count) {
     for (uint32_t r = 0; r < n; ++r) {
       const int rs = p.row_start[r], re = p.row_start[r + 1];
@@ -415,7 +416,8 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
     }
   };
   p.off_tiles = m.size();
-  tiles(attn_tile_queries(false), p.ntiles);
+  p.gq = attn_global_tile(p.row_start.data(), int(n), cfg.heads);
+  tiles(p.gq, p.ntiles);
   p.off_ltiles = m.size();
   tiles(attn_tile_queries(true), p.nltiles);
   const int per = 1 + int(kmax);
@@ -663,6 +665,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       at.ldo = d;
       at.scale = 1.0f / std::sqrt(float(cfg.head_dim()));
       at.window = L.local ? cfg.window() : -1;
+      at.tile_q = p.gq;
       attn_launch(at, stream);
     });
     x_ready = false;
@@ -709,7 +712,7 @@ void Model::run(const Plan& p, int kind, F&& enqueue) {
     hip_check(hipGetLastError(), "kernel launch");
     return;
   }
-  std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.ntiles, p.nltiles, p.nptiles, p.P, p.R, int64_t(p.off_ltiles),
+  std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.gq, p.ntiles, p.nltiles, p.nptiles, p.P, p.R, int64_t(p.off_ltiles),
                               int64_t(p.off_ids), int64_t(p.off_pos), int64_t(p.off_seg), int64_t(p.off_tiles),
                               int64_t(p.off_ptiles), int64_t(p.off_picked), int64_t(p.off_scorer),
                               int64_t(p.off_pooled), int64_t(reinterpret_cast<intptr_t>(amem)),
@@ -812,6 +815,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.out = a.att;
         at.tiles = tiles;
         at.ntiles = p.ntiles;
+        at.tile_q = p.gq;
         at.heads = cfg.head_nheads();
         at.Tq = T;
         at.Tk = T;
@@ -838,6 +842,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.out = a.attp;
         at.tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_ptiles);
         at.ntiles = p.nptiles;
+        at.tile_q = 128;  // picked-row tiles hold up to 128 slots
         at.qkey = picked;
         at.heads = cfg.head_nheads();
         at.Tq = T;

@@ -76,6 +76,7 @@ struct Plan {
   size_t off_ids = 0, off_pos = 0, off_seg = 0, off_tiles = 0, off_ltiles = 0, off_ptiles = 0, off_picked = 0,
          off_scorer = 0, off_pooled = 0;
   int ntiles = 0, nltiles = 0, nptiles = 0;
+  int gq = 256;  // queries per global-attention tile
 };
 
 struct Model {

@@ -218,9 +218,10 @@ def attention_ref(q, k, v, starts, window, scale):
     return out
 
 
-# window 64 and 16 take the staged local kernel, 100 the chunked one, -1 the global one
+# window 64 and 16 take the staged local kernel, 100 the chunked one, -1 the global one, whose
+# tiles hold 64 queries ([8, 200]), 128 (the other short batches) or 256 (24 rows of 600)
 @pytest.mark.parametrize("window", [-1, 64, 16, 100])
-@pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048], [5, 3, 250, 1, 700, 9]])
+@pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [2048], [5, 3, 250, 1, 700, 9], [600] * 24])
 def test_attention_varlen(dev, window, lens):
     say(f"attention window={window} lens={lens}")
     H = 16
