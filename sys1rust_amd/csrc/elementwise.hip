@@ -44,7 +44,7 @@ template <int PL>
 __global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restrict__ emb, const int* __restrict__ ids,
                                                       const float* __restrict__ w, float eps, int T, int d,
                                                       float* __restrict__ h, uint16_t* __restrict__ x) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
   const uint16_t* src = emb + size_t(ids[row]) * d;
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
                                                        float eps, int T, int d, uint16_t* __restrict__ yb,
                                                        float* __restrict__ yf, const float* __restrict__ addv,
                                                        const int* __restrict__ seg, float* __restrict__ yplus) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
   const int src_row = rows ? rows[row] : row;
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __res
                                                              const float* __restrict__ bias, float* __restrict__ h,
                                                              const float* __restrict__ w, float eps, int T, int d,
                                                              uint16_t* __restrict__ y) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
   const size_t plane = size_t(T) * d;
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void gather_f32_kernel(const float* __restrict
 
 __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
                                                     const float* __restrict__ b, int R, int d, float* __restrict__ out) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
   float acc = 0.0f;
@@ -297,14 +297,19 @@ __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict_
 
 }  // namespace
 
+// Row kernels run one wave per row, four rows per workgroup; a short batch (one request) takes one
+// row per workgroup instead, so its few rows spread over that many CUs rather than a quarter of them.
+inline int row_waves(int T) { return T < 2048 ? 1 : 4; }
+
 void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
                      uint16_t* x_out, hipStream_t st) {
   if (T <= 0) return;
-  dim3 grid((T + 3) / 4);
+  const int rw = row_waves(T);
+  dim3 grid((T + rw - 1) / rw), block(64 * rw);
   switch (d) {
-    case 512: hipLaunchKernelGGL(embed_ln_kernel<8>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
-    case 1024: hipLaunchKernelGGL(embed_ln_kernel<16>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
-    case 2048: hipLaunchKernelGGL(embed_ln_kernel<32>, grid, dim3(256), 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 512: hipLaunchKernelGGL(embed_ln_kernel<8>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 1024: hipLaunchKernelGGL(embed_ln_kernel<16>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 2048: hipLaunchKernelGGL(embed_ln_kernel<32>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
   }
 }
 
@@ -312,16 +317,17 @@ void layernorm_launch(const float* x, const int* rows, const float* w, const flo
                       uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
                       hipStream_t st) {
   if (T <= 0) return;
-  dim3 grid((T + 3) / 4);
+  const int rw = row_waves(T);
+  dim3 grid((T + rw - 1) / rw), block(64 * rw);
   switch (d) {
     case 512:
-      hipLaunchKernelGGL(layernorm_kernel<8>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
       break;
     case 1024:
-      hipLaunchKernelGGL(layernorm_kernel<16>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
       break;
     case 2048:
-      hipLaunchKernelGGL(layernorm_kernel<32>, grid, dim3(256), 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL(layernorm_kernel<32>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
       break;
   }
 }
@@ -329,16 +335,17 @@ void layernorm_launch(const float* x, const int* rows, const float* w, const flo
 void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T,
                             int d, uint16_t* y, hipStream_t st) {
   if (T <= 0) return;
-  dim3 grid((T + 3) / 4);
+  const int rw = row_waves(T);
+  dim3 grid((T + rw - 1) / rw), block(64 * rw);
   switch (d) {
     case 512:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<8>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<8>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
     case 1024:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<16>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<16>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
     case 2048:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<32>, grid, dim3(256), 0, st, ws, splits, bias, h, w, eps, T, d, y);
+      hipLaunchKernelGGL(splitk_resid_ln_kernel<32>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
   }
 }
