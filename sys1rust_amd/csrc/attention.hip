@@ -452,13 +452,193 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
 }
 
+
+// Global attention for a short batch (one request): a workgroup of KW waves takes 32 queries of
+// one row and head, and wave w visits the row's key chunks w, w + KW, ... with softmax statistics
+// of its own; the KW partial results merge through LDS at the end (the online-softmax
+// combination). A short row then runs KW times as many waves, each with 1/KW of the chain of
+// dependent chunks. Each wave stages its own chunks in a private 16 KiB of LDS (K rows and V^T
+// in the layouts attn_kernel uses), so the chunk loop has no barriers; the next chunk is loaded
+// into registers during this one's math and stored after it (a wave's LDS accesses run in
+// order), which keeps the workgroup at 64 KiB: two fit a CU.
+template <int KW>
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_ksplit_kernel(AttnArgs a) {
+  constexpr int REG = KC * 64;  // bf16 elements of one 8 KiB K or V^T chunk
+  // [wave] x (K | V^T); after the chunk loop the same memory holds the merge tables.
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[KW * 2 * REG];
+
+  const AttnTile tl = a.tiles[blockIdx.x];
+  const int head = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5, col = lane & 31;
+  const uint16_t* __restrict__ Qh = a.q + size_t(head) * a.Tq * 64;
+  const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.Tk * 64;
+  const uint16_t* __restrict__ Vt = a.v + size_t(head) * 64 * a.ldv;
+  uint16_t* const sK = smem + wave * 2 * REG;
+  uint16_t* const sVt = sK + REG;
+
+  const int qi = tl.q0 + col;
+  const bool qvalid = qi < tl.q1;
+  const int qld = min(qi, tl.q1 - 1);
+  const int qk = a.qkey ? a.qkey[qld] : qld;  // q row of this slot
+  const int kb0 = tl.k0, kb1 = tl.k1;
+  const int cstart = kb0 & ~7;
+  const int vlast = cstart + (((kb1 - 1) - cstart) & ~7);
+  bf16x8 qf[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+
+  // A chunk in registers: 16-byte piece p = lane + 64 it is K row p / 8, slot p % 8 (rows past
+  // kb1 repeat the last key), and V^T dim p / 8, keys 8 (p % 8) .. + 7 (from kb1 on, the piece
+  // holding key kb1 - 1; it may read up to 7 keys past kb1, the next sequence's or the zeros
+  // every v writer leaves up to the next multiple of 8 tokens).
+  uint4 kreg[8], vreg[8];
+  auto load = [&](int c0) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int p = lane + it * 64;
+      const int r = p >> 3, c = p & 7;
+      kreg[it] = *reinterpret_cast<const uint4*>(Kh + size_t(min(c0 + r, kb1 - 1)) * 64 + c * 8);
+      vreg[it] = *reinterpret_cast<const uint4*>(Vt + size_t(r) * a.ldv + min(c0 + c * 8, vlast));
+    }
+  };
+  auto store = [&] {  // K rows by kslot; V^T in the PV operand order of attn_kernel
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int p = lane + it * 64;
+      const int r = p >> 3, c = p & 7;
+      const uint4 kv = kreg[it];
+      *reinterpret_cast<uint4*>(sK + r * 64 + kslot(r, c) * 8) = make_uint4(kv.x, kv.y, kv.z, kv.w);
+      uint16_t* row = sVt + r * 64 + (c & 1) * 4;
+      *reinterpret_cast<uint2*>(row + kslot(r, c & ~1) * 8) = make_uint2(vreg[it].x, vreg[it].y);
+      *reinterpret_cast<uint2*>(row + kslot(r, c | 1) * 8) = make_uint2(vreg[it].z, vreg[it].w);
+    }
+  };
+
+  const float sl2 = a.scale * 1.4426950408889634f;
+  float m = NEG_INF, l = 0.0f;
+  f32x16 o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+
+  int c0 = cstart + wave * KC;
+  if (c0 < kb1) {
+    load(c0);
+    store();
+  }
+  for (; c0 < kb1; c0 += KW * KC) {
+    const bool more = c0 + KW * KC < kb1;
+    if (more) load(c0 + KW * KC);
+    const bool edge = c0 < kb0 || c0 + KC > kb1;
+    f32x16 s[2];
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[t][e] = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const int kr = t * 32 + col;
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+      }
+      if (edge) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = c0 + t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+          s[t][e] = key >= kb0 && key < kb1 ? s[t][e] : NEG_INF;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx * sl2);
+    const float ms = mn == NEG_INF ? 0.0f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - ms);
+    float psum = 0.0f;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
+          psum += p;
+          pf[t][sb][j] = __bf16(p);
+        }
+    l = l * alpha + psum;
+    m = mn;
+    if (alpha != 1.0f) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const int dr = dt * 32 + col;
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sVt + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+        }
+    if (more) store();  // after this chunk's reads
+  }
+
+  // Merge: wave w leaves (m, l, o) per lane in LDS; wave 0 combines them. A wave that visited no
+  // chunk has m = -inf and contributes 0.
+  const float lw = l + __shfl_xor(l, 32, 64);
+  __syncthreads();  // every wave is done with its chunk buffers
+  float* mt = reinterpret_cast<float*>(smem);  // [KW][64] m, [KW][64] l, [KW][32][64] o
+  float* lt = mt + KW * 64;
+  float* ot = lt + KW * 64;
+  mt[wave * 64 + lane] = m;
+  lt[wave * 64 + lane] = lw;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) ot[(wave * 32 + e) * 64 + lane] = o[e >> 4][e & 15];
+  __syncthreads();
+  if (wave != 0 || !qvalid) return;
+  float M = NEG_INF;
+#pragma unroll
+  for (int w = 0; w < KW; ++w) M = fmaxf(M, mt[w * 64 + lane]);
+  float f[KW], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    const float mw = mt[w * 64 + lane];
+    f[w] = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+    L += lt[w * 64 + lane] * f[w];
+  }
+  const float inv = 1.0f / L;
+  uint16_t* orow = a.out + size_t(qi) * a.ldo + head * 64;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = dt * 16 + g * 4 + r;
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) acc += ot[(w * 32 + e) * 64 + lane] * f[w];
+        v[r] = acc * inv;
+      }
+      const int dim = dt * 32 + g * 8 + hl * 4;
+      *reinterpret_cast<uint2*>(orow + dim) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+    }
+}
+
 }  // namespace
 
 int attn_tile_queries(bool local) { return local ? LQ : 256; }
 
 // 256-query tiles (8 waves, every K/V chunk shared by 256 queries) while they give at least one
-// workgroup per CU; a short request instead takes 128 or 64 (fewer queries per K/V chunk, but
-// more of the 256 CUs at work): the first that gives 128 workgroups, else 64.
+// workgroup per CU; then 128 (4 waves) while they give 128 workgroups; a shorter batch takes
+// 32-query tiles whose keys are split over 4 waves (attn_ksplit_kernel).
 int attn_global_tile(const int* row_start, int n, int heads) {
   auto count = [&](int qb) {
     long long c = 0;
@@ -466,7 +646,8 @@ int attn_global_tile(const int* row_start, int n, int heads) {
     return c * heads;
   };
   if (count(256) >= 256) return 256;
-  return count(128) >= 128 ? 128 : 64;
+  if (count(128) >= 128) return 128;
+  return 32;  // attn_ksplit_kernel
 }
 
 void attn_launch(const AttnArgs& a, hipStream_t st) {
@@ -480,8 +661,10 @@ void attn_launch(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_kernel<false, 8>), grid, dim3(512), 0, st, a);
   else if (a.tile_q == 128)
     hipLaunchKernelGGL((attn_kernel<false, 4>), grid, dim3(256), 0, st, a);
+  else if (a.key_waves == 8)  // tile_q 32
+    hipLaunchKernelGGL((attn_ksplit_kernel<8>), grid, dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(128), 0, st, a);
+    hipLaunchKernelGGL((attn_ksplit_kernel<4>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace s1

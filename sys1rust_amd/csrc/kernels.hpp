@@ -60,7 +60,7 @@ inline int vt_ld(int T) { return (T + 7) / 8 * 8 + 64; }
 
 // Attention over packed variable-length rows. q, k are [H, Tq or Tk, 64] bf16 (head-major) and v
 // is transposed, [H, 64, ldv] (vt_ld(Tk)).
-// Queries are numbered by output slot; each work tile is up to 128 consecutive slots of one
+// Queries are numbered by output slot; each work tile is up to tile_q consecutive slots of one
 // sequence: {q0, q1, k0, k1} = slots [q0, q1) and the sequence's key range [k0, k1). Slot s reads
 // q row qkey[s] (or s when qkey is null), writes out row s, and sits at key index qkey[s] for
 // the window test. The decision head's pruned last layer uses qkey to attend from a few picked
@@ -82,11 +82,14 @@ struct AttnArgs {
   int ldo = 0;
   float scale = 0.125f;
   int window = -1;  // < 0: global attention; else keys with |i - j| <= window
-  int tile_q = 256;  // global attention: the tiles' query count, 256, 128 or 64 (8, 4 or 2 waves)
+  // Global attention: queries per tile, 256 or 128 (8 or 4 waves, each with 32 queries and every
+  // key), or 32: then key_waves (4 or 8) waves split each tile's keys.
+  int tile_q = 256;
+  int key_waves = 4;
 };
 void attn_launch(const AttnArgs& a, hipStream_t st);
-// Queries per work tile the attention kernel takes: 128 on local layers; on global layers the
-// largest of 256, 128 and 64 that still gives the GPU enough workgroups, given the rows' lengths.
+// Queries per work tile the attention kernel takes: 128 on local layers; on global layers 256 or
+// 128 when that still gives the GPU enough workgroups, given the rows' lengths, else 32.
 int attn_tile_queries(bool local);
 int attn_global_tile(const int* row_start, int n, int heads);
 

@@ -401,7 +401,7 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
   };
   pad4();
   // Attention work tiles: query blocks of one row; for global layers 256 queries (one workgroup
-  // of 8 waves), or 128 / 64 for a short batch (attn_global_tile); 128 for local ones (4 waves;
+  // of 8 waves), or 128 or 32 for a short batch (attn_global_tile); 128 for local ones (4 waves;
   // their keys are only the window).
   auto tiles = [&](int qb, int& count) {
     for (uint32_t r = 0; r < n; ++r) {
@@ -842,7 +842,10 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.out = a.attp;
         at.tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_ptiles);
         at.ntiles = p.nptiles;
-        at.tile_q = 128;  // picked-row tiles hold up to 128 slots
+        // A row's picked slots are one tile (up to 128); up to 32 of them take 8 waves that
+        // split the keys, since these tiles are few.
+        at.tile_q = 1 + p.kmax <= 32 ? 32 : 128;
+        at.key_waves = 8;
         at.qkey = picked;
         at.heads = cfg.head_nheads();
         at.Tq = T;
