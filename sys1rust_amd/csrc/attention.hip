@@ -44,6 +44,16 @@ constexpr float NEG_INF = -__builtin_huge_valf();
 // load (global_load_lds_dwordx4) fills.
 __device__ __forceinline__ int kslot(int r, int c) { return c ^ ((r >> 1) & 7); }
 
+// The launch is one-dimensional, ntiles x heads workgroups; workgroup -> (tile, head) with the
+// tile fastest, through xcd_remap, so that consecutive tiles of one head (the query blocks of one
+// row, which read the same keys and values, or overlapping windows of them) run on one XCD and
+// share its L2.
+__device__ __forceinline__ int2 tile_head(int ntiles) {
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int head = lid / ntiles;
+  return make_int2(lid - head * ntiles, head);
+}
+
 // Three waves per SIMD for the local kernel (register budget 168), four for the global one.
 template <bool LOCAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
@@ -53,8 +63,9 @@ void attn_kernel(AttnArgs a) {
   auto sK = [&](int buf) { return smem + buf * KC * 64; };
   auto sVt = [&](int buf) { return smem + (2 + buf) * KC * 64; };
 
-  const AttnTile tl = a.tiles[blockIdx.x];
-  const int head = blockIdx.y;
+  const int2 th = tile_head(a.ntiles);
+  const AttnTile tl = a.tiles[th.x];
+  const int head = th.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int hl = lane >> 5;   // lane half
@@ -297,8 +308,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   __shared__ __attribute__((aligned(1024))) uint16_t sK[LMAXK * 64];
   __shared__ __attribute__((aligned(1024))) uint16_t sVt[64 * LVW];
 
-  const AttnTile tl = a.tiles[blockIdx.x];
-  const int head = blockIdx.y;
+  const int2 th = tile_head(a.ntiles);
+  const AttnTile tl = a.tiles[th.x];
+  const int head = th.y;
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform values go through readfirstlane so the branches on them are scalar branches,
   // not exec-mask regions around every tile.
@@ -467,8 +479,9 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   // [wave] x (K | V^T); after the chunk loop the same memory holds the merge tables.
   __shared__ __attribute__((aligned(1024))) uint16_t smem[KW * 2 * REG];
 
-  const AttnTile tl = a.tiles[blockIdx.x];
-  const int head = blockIdx.y;
+  const int2 th = tile_head(a.ntiles);
+  const AttnTile tl = a.tiles[th.x];
+  const int head = th.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, col = lane & 31;
@@ -652,7 +665,7 @@ int attn_global_tile(const int* row_start, int n, int heads) {
 
 void attn_launch(const AttnArgs& a, hipStream_t st) {
   if (a.ntiles <= 0) return;
-  dim3 grid(a.ntiles, a.heads);
+  const dim3 grid(a.ntiles * a.heads);
   if (a.window >= 0 && a.window <= LMAXW && !a.qkey)
     hipLaunchKernelGGL(attn_local_kernel, grid, dim3(256), 0, st, a);  // tiles of <= LQ queries
   else if (a.window >= 0)
