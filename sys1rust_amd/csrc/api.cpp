@@ -380,9 +380,10 @@ int s1k_attention(const void* q, const void* k, const void* v, int v_ld, int T, 
     std::vector<int> tiles;
     for (int r = 0; r < nseq; ++r) {
       const int rs = seq_starts[r], re = seq_starts[r + 1];
-      for (int q0 = rs; q0 < re; q0 += qb) {
+      const int step = s1::attn_row_step(re - rs, qb);
+      for (int q0 = rs; q0 < re; q0 += step) {
         tiles.push_back(q0);
-        tiles.push_back(std::min(q0 + qb, re));
+        tiles.push_back(std::min(q0 + step, re));
         tiles.push_back(rs);
         tiles.push_back(re);
       }

@@ -28,6 +28,8 @@
 // below 2^-126 to 0, weights far below anything the f32 sums or the bf16 P can hold next to the
 // row maximum's 1. exp2f wraps the instruction in a denormal-range fixup of five more VALU
 // instructions per weight, and these kernels are VALU-bound.
+#include <algorithm>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -648,6 +650,12 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 }  // namespace
 
 int attn_tile_queries(bool local) { return local ? LQ : 256; }
+
+int attn_row_step(int len, int qb) {
+  if (qb <= 32) return qb;
+  const int nt = (len + qb - 1) / qb;
+  return std::min(qb, ((len + nt - 1) / nt + 31) / 32 * 32);
+}
 
 // 256-query tiles (8 waves, every K/V chunk shared by 256 queries) while they give at least one
 // workgroup per CU; then 128 (4 waves) while they give 128 workgroups; a shorter batch takes

@@ -92,6 +92,10 @@ void attn_launch(const AttnArgs& a, hipStream_t st);
 // 128 when that still gives the GPU enough workgroups, given the rows' lengths, else 32.
 int attn_tile_queries(bool local);
 int attn_global_tile(const int* row_start, int n, int heads);
+// The query step that cuts a row of len tokens into tiles of at most qb queries: as many tiles
+// as qb needs, of even sizes rounded up to whole waves (570 tokens at 256: 192, 192, 186), so a
+// row's last tile is not a nearly idle workgroup beside full ones.
+int attn_row_step(int len, int qb);
 
 // h[t] = LN(tok_emb[ids[t]]) (no bias), written as f32 and as bf16.
 void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,

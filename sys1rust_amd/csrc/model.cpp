@@ -406,9 +406,10 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
   auto tiles = [&](int qb, int& count) {
     for (uint32_t r = 0; r < n; ++r) {
       const int rs = p.row_start[r], re = p.row_start[r + 1];
-      for (int q0 = rs; q0 < re; q0 += qb) {
+      const int step = attn_row_step(re - rs, qb);
+      for (int q0 = rs; q0 < re; q0 += step) {
         m.push_back(q0);
-        m.push_back(std::min(q0 + qb, re));
+        m.push_back(std::min(q0 + step, re));
         m.push_back(rs);
         m.push_back(re);
         ++count;
