@@ -231,46 +231,52 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
     const int rl0 = wm * TM + l32;        // the same row and column, local to the tile
     const int cl0 = wn * TN + 4 * h;
     const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (g.splits > 1) {
-      // Split-K: this k-range's partial tile goes to ws[split] as f32; splitk_epilogue_kernel
-      // sums the splits and applies the epilogue.
-      float* part = g.ws + size_t(split) * g.M * g.N;
+    if constexpr (EPI == EPI_RESID || EPI == EPI_F32) {
+      // f32 out: with split-K (which gemm_launch always runs with this epilogue) this k-range's
+      // partial tile into ws[split], summed in split order by splitk_epilogue_kernel or
+      // splitk_resid_ln_kernel; else C (+)= acc + bias. The tile leaves through LDS like the bf16
+      // results: staged [rows][BN] (rows padded by 16 bytes), then written as whole rows, 16 bytes
+      // per lane and BN / 4 lanes per row, so every access covers whole cache lines (straight
+      // from the fragments an access is a 32-byte piece of each of 32 rows).
+      const bool part = g.splits > 1;
+      float* out = part ? g.ws + size_t(split) * g.M * g.N : reinterpret_cast<float*>(g.C);
+      const int ld = part ? g.N : g.ldc;
+      constexpr int PF = BN * 4 + 16;
+      constexpr int NHF = BM * PF <= STAGES * STAGE_BYTES ? 1 : 2;
+      constexpr int HRF = BM / NHF;
+      static_assert(HRF * PF <= STAGES * STAGE_BYTES && HRF % 32 == 0, "f32 staging must fit the stage buffers");
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = rbase + i * 32;
-        if (row >= g.M) continue;
+      for (int half = 0; half < NHF; ++half) {
+        __syncthreads();
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<float4*>(part + size_t(row) * g.N + cbase + j * 32 + q * 8) =
-                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-      }
-      return;
-    }
-    if constexpr (EPI == EPI_RESID || EPI == EPI_F32) {
-      // f32 C (+)= acc + bias, 16 bytes per lane access.
+          for (int q = 0; q < 4; ++q) {
+            const int col = cbase + j * 32 + q * 8;
+            const float4 b = !part && g.bias ? *reinterpret_cast<const float4*>(g.bias + col) : zero4;
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = cbase + j * 32 + q * 8;
-          const float4 b = g.bias ? *reinterpret_cast<const float4*>(g.bias + col) : zero4;
-#pragma unroll
-          for (int i = 0; i < FM; ++i) {
-            const int row = rbase + i * 32;
-            if (row >= g.M) continue;
-            float4* c = reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + size_t(row) * g.ldc + col);
-            const float4 v = make_float4(acc[i][j][4 * q] + b.x, acc[i][j][4 * q + 1] + b.y,
-                                         acc[i][j][4 * q + 2] + b.z, acc[i][j][4 * q + 3] + b.w);
-            if constexpr (EPI == EPI_RESID) {
-              const float4 old = *c;
-              *c = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
-            } else {
-              *c = v;
+            for (int i = 0; i < FM; ++i) {
+              if ((wm * TM + i * 32) / HRF != half) continue;
+              *reinterpret_cast<float4*>(stg + (rl0 + i * 32 - half * HRF) * PF + (cl0 + j * 32 + q * 8) * 4) =
+                  make_float4(acc[i][j][4 * q] + b.x, acc[i][j][4 * q + 1] + b.y, acc[i][j][4 * q + 2] + b.z,
+                              acc[i][j][4 * q + 3] + b.w);
             }
           }
+        __syncthreads();
+        for (int idx = tid; idx < HRF * (BN / 4); idx += NT) {
+          const int r = idx / (BN / 4), c4 = idx % (BN / 4);
+          const int row = m0 + half * HRF + r;
+          if (row >= g.M) continue;
+          const float4 v = *reinterpret_cast<const float4*>(stg + r * PF + c4 * 16);
+          float4* c = reinterpret_cast<float4*>(out + size_t(row) * ld + n0 + c4 * 4);
+          if (EPI == EPI_RESID && !part) {
+            const float4 old = *c;
+            *c = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+          } else {
+            *c = v;
+          }
         }
+      }
       return;
     } else if constexpr (EPI == EPI_GEGLU) {
       // W rows interleaved by 32: fragment 2p is x, 2p + 1 its gate; output columns
