@@ -278,7 +278,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": round(ms / BASELINE_M5_10Q512_MS, 5),
-        "dtype": "bf16",
+        "dtype": "f16" if model.name().endswith(",f16)") else "bf16",
         "data": "synthetic",
         "config": {"workload": f"{args.workload}: encoder+head+scorer forward and answer decode, ModernBERT-large "
                                f"shape, random-init bf16 weights",

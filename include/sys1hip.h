@@ -38,7 +38,10 @@ typedef struct s1_model s1_model;
  * `encoder_config_json`: encoder/config.json text (EncoderConfig::from_value, config.rs:96-159).
  * `agent_config_json`: rl_agent_config.json text or NULL (AgentConfig, config.rs:9-40).
  * `settings`: strict comma list like BackendOptions::tuning (backend.rs:22-32); an unknown key is
- * S1_ERR_CONFIG (Knobs::parse, lib.rs:155-259). NULL or "" selects the defaults. */
+ * S1_ERR_CONFIG (Knobs::parse, lib.rs:155-259). NULL or "" selects the defaults. `dtype=f16`
+ * keeps weights and activations in f16, the checkpoints' own type (BackendOptions::f32 = false,
+ * backend.rs:25-27, keeps the checkpoint's f16 weights); the default `dtype=bf16` rounds them to
+ * bf16. Accumulation, LayerNorm, softmax and the residual stream are f32 either way. */
 int s1_model_create(const char* safetensors_path, const char* encoder_config_json,
                     const char* agent_config_json, const char* settings, int device_ordinal,
                     s1_model** out);

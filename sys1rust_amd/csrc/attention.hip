@@ -57,9 +57,10 @@ __device__ __forceinline__ int2 tile_head(int ntiles) {
 }
 
 // Three waves per SIMD for the local kernel (register budget 168), four for the global one.
-template <bool LOCAL, int NW>
+template <class E, bool LOCAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LOCAL ? 3 : 4)))
 void attn_kernel(AttnArgs a) {
+  typedef typename E::v8 v8;
   // K and V^T double buffers, [K0 | K1 | V0 | V1], 8 KiB each.
   __shared__ __attribute__((aligned(1024))) uint16_t smem[4 * KC * 64];
   auto sK = [&](int buf) { return smem + buf * KC * 64; };
@@ -108,10 +109,10 @@ void attn_kernel(AttnArgs a) {
   const int cstart = kb0 & ~7;
 
   // This lane's slice of its query: dims 16kb + 8h .. +7 for kb = 0..3 (MFMA B operand).
-  bf16x8 qf[4];
+  v8 qf[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
-    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+    qf[kb] = *reinterpret_cast<const v8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
 
   // A chunk's K goes global -> LDS by direct loads: 8 groups of 8 rows, one KiB each, spread
   // over the waves; rows past kb1 repeat the last key. V^T goes through registers (one 16-byte
@@ -209,8 +210,8 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
           const int kr = t * 32 + col;
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK(buf) + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
-          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+          const v8 kf = *reinterpret_cast<const v8*>(sK(buf) + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
+          s[t] = E::mfma(kf, qf[kb], s[t]);
         }
         if (edge) {
 #pragma unroll
@@ -230,7 +231,7 @@ void attn_kernel(AttnArgs a) {
       const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is exp2(-inf) = 0
       const float alpha = __builtin_amdgcn_exp2f(m - ms);
       float psum = 0.0f;
-      bf16x8 pf[2][2];
+      v8 pf[2][2];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -239,7 +240,7 @@ void attn_kernel(AttnArgs a) {
           for (int j = 0; j < 8; ++j) {
             const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
             psum += p;
-            pf[t][sb][j] = __bf16(p);
+            pf[t][sb][j] = typename E::scalar(p);
           }
       l = l * alpha + psum;
       m = mn;
@@ -259,8 +260,8 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
           for (int dt = 0; dt < 2; ++dt) {
             const int dr = dt * 32 + col;
-            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sVt(buf) + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+            const v8 vf = *reinterpret_cast<const v8*>(sVt(buf) + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
+            o[dt] = E::mfma(vf, pf[t][sb], o[dt]);
           }
         }
       }
@@ -285,8 +286,8 @@ void attn_kernel(AttnArgs a) {
     for (int g = 0; g < 4; ++g) {
       const int dim = dt * 32 + g * 8 + hl * 4;
       uint2 w;
-      w.x = pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
-      w.y = pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
+      w.x = E::pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
+      w.y = E::pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
       *reinterpret_cast<uint2*>(orow + dim) = w;
     }
 }
@@ -306,7 +307,9 @@ constexpr int LVW = LVC * 8;
 constexpr int LTILES = (32 + 2 * LMAXW + 7 + 31) / 32;  // 32-key tiles a wave's window spans
 static_assert(LVC % 2 == 1 && LVC * 8 >= (LMAXK + 31) / 32 * 32 && 64 * LVC % 64 == 0, "V^T layout");
 
+template <class E>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_local_kernel(AttnArgs a) {
+  typedef typename E::v8 v8;
   __shared__ __attribute__((aligned(1024))) uint16_t sK[LMAXK * 64];
   __shared__ __attribute__((aligned(1024))) uint16_t sVt[64 * LVW];
 
@@ -365,10 +368,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int qi = wq0 + col;
   const bool qvalid = qi < tl.q1;
   const int qk = min(qi, tl.q1 - 1);
-  bf16x8 qf[4];
+  v8 qf[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
-    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+    qf[kb] = *reinterpret_cast<const v8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
 
   // This wave's window: keys [ws, we) cover every query's |key - q| <= W within the row.
   const int ws = max(kb0, wq0 - W), we = min(kb1, min(wq0 + 31, tl.q1 - 1) + W + 1);
@@ -397,8 +400,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int kr = t0 + t * 32 + col;
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[kr * 64 + kslot(kr, kb * 2 + hl) * 8]);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], acc, 0, 0, 0);
+      const v8 kf = *reinterpret_cast<const v8*>(&sK[kr * 64 + kslot(kr, kb * 2 + hl) * 8]);
+      acc = E::mfma(kf, qf[kb], acc);
     }
     const int tb = t0 + t * 32;  // LDS key offset of the tile
     if (tb >= blo && tb + 32 <= bhi) {
@@ -427,14 +430,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
   for (int t = 0; t < LTILES; ++t) {
     if (t >= nt) continue;
-    bf16x8 pf[2];
+    v8 pf[2];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
         psum += p;
-        pf[sb][j] = __bf16(p);
+        pf[sb][j] = typename E::scalar(p);
       }
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -445,8 +448,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         const uint2 lo = *reinterpret_cast<const uint2*>(vr + kbase);
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + kbase + 8);
         const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&pk);
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[sb], o[dt], 0, 0, 0);
+        const v8 vf = *reinterpret_cast<const v8*>(&pk);
+        o[dt] = E::mfma(vf, pf[sb], o[dt]);
       }
     }
   }
@@ -460,8 +463,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     for (int g = 0; g < 4; ++g) {
       const int dim = dt * 32 + g * 8 + hl * 4;
       uint2 w;
-      w.x = pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
-      w.y = pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
+      w.x = E::pack2(o[dt][g * 4 + 0] * inv, o[dt][g * 4 + 1] * inv);
+      w.y = E::pack2(o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv);
       *reinterpret_cast<uint2*>(orow + dim) = w;
     }
 }
@@ -475,8 +478,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 // in the layouts attn_kernel uses), so the chunk loop has no barriers; the next chunk is loaded
 // into registers during this one's math and stored after it (a wave's LDS accesses run in
 // order), which keeps the workgroup at 64 KiB: two fit a CU.
-template <int KW>
+template <class E, int KW>
 __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_ksplit_kernel(AttnArgs a) {
+  typedef typename E::v8 v8;
   constexpr int REG = KC * 64;  // bf16 elements of one 8 KiB K or V^T chunk
   // [wave] x (K | V^T); after the chunk loop the same memory holds the merge tables.
   __shared__ __attribute__((aligned(1024))) uint16_t smem[KW * 2 * REG];
@@ -500,10 +504,10 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int kb0 = tl.k0, kb1 = tl.k1;
   const int cstart = kb0 & ~7;
   const int vlast = cstart + (((kb1 - 1) - cstart) & ~7);
-  bf16x8 qf[4];
+  v8 qf[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
-    qf[kb] = *reinterpret_cast<const bf16x8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
+    qf[kb] = *reinterpret_cast<const v8*>(Qh + size_t(qk) * 64 + kb * 16 + hl * 8);
 
   // A chunk in registers: 16-byte piece p = lane + 64 it is K row p / 8, slot p % 8 (rows past
   // kb1 repeat the last key), and V^T dim p / 8, keys 8 (p % 8) .. + 7 (from kb1 on, the piece
@@ -556,8 +560,8 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         const int kr = t * 32 + col;
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s[t], 0, 0, 0);
+        const v8 kf = *reinterpret_cast<const v8*>(sK + kr * 64 + kslot(kr, kb * 2 + hl) * 8);
+        s[t] = E::mfma(kf, qf[kb], s[t]);
       }
       if (edge) {
 #pragma unroll
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const float ms = mn == NEG_INF ? 0.0f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ms);
     float psum = 0.0f;
-    bf16x8 pf[2][2];
+    v8 pf[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -583,7 +587,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int j = 0; j < 8; ++j) {
           const float p = __builtin_amdgcn_exp2f(fmaf(s[t][sb * 8 + j], sl2, -ms));
           psum += p;
-          pf[t][sb][j] = __bf16(p);
+          pf[t][sb][j] = typename E::scalar(p);
         }
     l = l * alpha + psum;
     m = mn;
@@ -598,8 +602,8 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt) {
           const int dr = dt * 32 + col;
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sVt + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][sb], o[dt], 0, 0, 0);
+          const v8 vf = *reinterpret_cast<const v8*>(sVt + dr * 64 + kslot(dr, (t * 2 + sb) * 2 + hl) * 8);
+          o[dt] = E::mfma(vf, pf[t][sb], o[dt]);
         }
     if (more) store();  // after this chunk's reads
   }
@@ -643,7 +647,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         v[r] = acc * inv;
       }
       const int dim = dt * 32 + g * 8 + hl * 4;
-      *reinterpret_cast<uint2*>(orow + dim) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+      *reinterpret_cast<uint2*>(orow + dim) = make_uint2(E::pack2(v[0], v[1]), E::pack2(v[2], v[3]));
     }
 }
 
@@ -671,21 +675,27 @@ int attn_global_tile(const int* row_start, int n, int heads) {
   return 32;  // attn_ksplit_kernel
 }
 
-void attn_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.ntiles <= 0) return;
+template <class E>
+void attn_launch_t(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.ntiles * a.heads);
   if (a.window >= 0 && a.window <= LMAXW && !a.qkey)
-    hipLaunchKernelGGL(attn_local_kernel, grid, dim3(256), 0, st, a);  // tiles of <= LQ queries
+    hipLaunchKernelGGL(attn_local_kernel<E>, grid, dim3(256), 0, st, a);  // tiles of <= LQ queries
   else if (a.window >= 0)
-    hipLaunchKernelGGL((attn_kernel<true, 4>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<E, true, 4>), grid, dim3(256), 0, st, a);
   else if (a.tile_q == 256)
-    hipLaunchKernelGGL((attn_kernel<false, 8>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<E, false, 8>), grid, dim3(512), 0, st, a);
   else if (a.tile_q == 128)
-    hipLaunchKernelGGL((attn_kernel<false, 4>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<E, false, 4>), grid, dim3(256), 0, st, a);
   else if (a.key_waves == 8)  // tile_q 32
-    hipLaunchKernelGGL((attn_ksplit_kernel<8>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((attn_ksplit_kernel<E, 8>), grid, dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_ksplit_kernel<4>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_ksplit_kernel<E, 4>), grid, dim3(256), 0, st, a);
+}
+
+void attn_launch(const AttnArgs& a, hipStream_t st) {
+  if (a.ntiles <= 0) return;
+  if (a.elem == ELEM_F16) attn_launch_t<F16>(a, st);
+  else attn_launch_t<Bf16>(a, st);
 }
 
 }  // namespace s1

@@ -174,5 +174,26 @@ inline float f16_to_f32(uint16_t h) {
   std::memcpy(&f, &u, 4);
   return f;
 }
+// f32 -> f16, round to nearest even; overflow goes to infinity, NaN stays a (quiet) NaN.
+inline uint16_t f32_to_f16(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint16_t sign = uint16_t((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return uint16_t(sign | 0x7e00u);
+  if (ax >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // >= 65520 rounds past 65504
+  if (ax < 0x38800000u) {                                  // below 2^-14: a subnormal f16, units of 2^-24
+    const int e = int(ax >> 23);
+    const int shift = 126 - e;
+    if (e == 0 || shift > 24) return sign;
+    const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t q = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return uint16_t(sign | q);
+  }
+  const uint32_t r = ax + 0xfffu + ((ax >> 13) & 1u) - ((127u - 15u) << 23);
+  return uint16_t(sign | (r >> 13));
+}
 
 }  // namespace s1

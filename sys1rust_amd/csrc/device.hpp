@@ -27,19 +27,53 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Unpack 8 bf16 held in a uint4 to floats.
+// The 16-bit element type of weights and activations, a template parameter of every kernel that
+// touches them: bf16 (the default) or f16 (the checkpoints' own type, setting dtype=f16). Both
+// feed the 32x32x16 MFMA at the same rate; the traits give the MFMA opcode and the conversions
+// (f32 -> 16 bit rounds to nearest even, v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+struct Bf16 {
+  typedef __bf16 scalar;
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float f32(uint16_t h) { return bf2f(h); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return s1::pack2(a, b); }
+  static __device__ __forceinline__ uint16_t bits(float f) { return f2bf(f); }
+};
+struct F16 {
+  typedef _Float16 scalar;
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    v2 r;
+    r[0] = static_cast<_Float16>(a);
+    r[1] = static_cast<_Float16>(b);
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+};
+
+// 8 elements of type E held in a uint4 <-> floats.
+template <class E>
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
-  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
-  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
-  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
-  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = E::f32(uint16_t(w[i]));
+    f[2 * i + 1] = E::f32(uint16_t(w[i] >> 16));
+  }
 }
-
+template <class E>
 __device__ __forceinline__ uint4 pack8(const float* f) {
-  return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+  return make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
 }
 
-// The first `valid` (0..8) bf16 elements of an 8-element piece, the rest zeroed, by selects.
+// The first `valid` (0..8) 16-bit elements of an 8-element piece, the rest zeroed, by selects.
 __device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
   auto m = [valid](int e) { return (valid > e ? 0x0000ffffu : 0u) | (valid > e + 1 ? 0xffff0000u : 0u); };
   v.x &= m(0);

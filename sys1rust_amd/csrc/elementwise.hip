@@ -40,7 +40,7 @@ __device__ __forceinline__ void ln_stats(const float* v, int d, float eps, float
 }
 
 // Lane l owns elements [8l + 512c, 8l + 512c + 8) for c = 0 .. PL/8 - 1.
-template <int PL>
+template <class E, int PL>
 __global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restrict__ emb, const int* __restrict__ ids,
                                                       const float* __restrict__ w, float eps, int T, int d,
                                                       float* __restrict__ h, uint16_t* __restrict__ x) {
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restric
 #pragma unroll
   for (int c = 0; c < PL / 8; ++c) {
     const uint4 u = *reinterpret_cast<const uint4*>(src + c * 512 + lane * 8);
-    unpack8(u, v + c * 8);
+    unpack8<E>(u, v + c * 8);
   }
   float mean, rstd;
   ln_stats<PL>(v, d, eps, mean, rstd);
@@ -66,11 +66,11 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const uint16_t* __restric
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = (v[c * 8 + e] - mean) * rstd * wv[c * 8 + e];
     store8f(h + size_t(row) * d + o, y);
-    *reinterpret_cast<uint4*>(x + size_t(row) * d + o) = pack8(y);
+    *reinterpret_cast<uint4*>(x + size_t(row) * d + o) = pack8<E>(y);
   }
 }
 
-template <int PL>
+template <class E, int PL>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, const int* __restrict__ rows,
                                                        const float* __restrict__ w, const float* __restrict__ b,
                                                        float eps, int T, int d, uint16_t* __restrict__ yb,
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   if (yb) {
 #pragma unroll
     for (int c = 0; c < PL / 8; ++c)
-      *reinterpret_cast<uint4*>(yb + size_t(row) * d + c * 512 + lane * 8) = pack8(y + c * 8);
+      *reinterpret_cast<uint4*>(yb + size_t(row) * d + c * 512 + lane * 8) = pack8<E>(y + c * 8);
   }
   if (yf) {
 #pragma unroll
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 // order from 0.0f, then the bias (or 0.0f), then onto h: the arithmetic of the GEMM's split-K
 // epilogue; the statistics and y are layernorm_kernel's on the new h. The splits are loaded SG
 // at a time, all in flight together, so the row waits on ceil(splits / SG) load rounds.
-template <int PL, int SG = 32 / PL * 4>
+template <class E, int PL, int SG = 32 / PL * 4>
 __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __restrict__ ws, int splits,
                                                              const float* __restrict__ bias, float* __restrict__ h,
                                                              const float* __restrict__ w, float eps, int T, int d,
@@ -181,11 +181,12 @@ __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __res
   for (int i = 0; i < PL; ++i) o[i] = (v[i] - mean) * rstd * wv[i] + 0.0f;
 #pragma unroll
   for (int c = 0; c < PL / 8; ++c)
-    *reinterpret_cast<uint4*>(y + size_t(row) * d + c * 512 + lane * 8) = pack8(o + c * 8);
+    *reinterpret_cast<uint4*>(y + size_t(row) * d + c * 512 + lane * 8) = pack8<E>(o + c * 8);
 }
 
 // One thread per (token, head, quarter of the 32 rotation pairs): pairs i0 .. i0 + 7 with
 // i0 = 8 * quarter, i.e. dims [i0, i0 + 8) and [i0 + 32, i0 + 40) of the head, for q, k and v.
+template <class E>
 __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restrict__ qkv, int T, int d,
                                                         const int* __restrict__ pos, const float* __restrict__ ct,
                                                         const float* __restrict__ stab, uint16_t* __restrict__ q,
@@ -222,15 +223,15 @@ __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restr
       continue;
     }
     float x1[8], x2[8], y1[8], y2[8];
-    unpack8(a, x1);
-    unpack8(b, x2);
+    unpack8<E>(a, x1);
+    unpack8<E>(b, x2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       y1[j] = x1[j] * c[j] - x2[j] * s[j];
       y2[j] = x1[j] * s[j] + x2[j] * c[j];
     }
-    *reinterpret_cast<uint4*>(dp) = pack8(y1);
-    *reinterpret_cast<uint4*>(dp + 32) = pack8(y2);
+    *reinterpret_cast<uint4*>(dp) = pack8<E>(y1);
+    *reinterpret_cast<uint4*>(dp + 32) = pack8<E>(y2);
   }
   // v, transposed: dims i0 .. i0 + 7 and i0 + 32 .. i0 + 39 of token t.
   const uint16_t* sv = src + 2 * d;
@@ -254,6 +255,7 @@ __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restr
       }
 }
 
+template <class E>
 __global__ __launch_bounds__(256) void geglu_kernel(const uint16_t* __restrict__ wi, int T, int I,
                                                    uint16_t* __restrict__ act) {
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -262,11 +264,11 @@ __global__ __launch_bounds__(256) void geglu_kernel(const uint16_t* __restrict__
   const int t = int(gid / per_row), c = int(gid % per_row) * 8;
   const uint16_t* r = wi + size_t(t) * 2 * I;
   float x[8], g[8], y[8];
-  unpack8(*reinterpret_cast<const uint4*>(r + c), x);
-  unpack8(*reinterpret_cast<const uint4*>(r + I + c), g);
+  unpack8<E>(*reinterpret_cast<const uint4*>(r + c), x);
+  unpack8<E>(*reinterpret_cast<const uint4*>(r + I + c), g);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = gelu_erf(x[e]) * g[e];
-  *reinterpret_cast<uint4*>(act + size_t(t) * I + c) = pack8(y);
+  *reinterpret_cast<uint4*>(act + size_t(t) * I + c) = pack8<E>(y);
 }
 
 __global__ __launch_bounds__(256) void gather_f32_kernel(const float* __restrict__ x, const int* __restrict__ rows,
@@ -278,6 +280,7 @@ __global__ __launch_bounds__(256) void gather_f32_kernel(const float* __restrict
   for (int i = threadIdx.x; i < d / 4; i += 256) o[i] = s[i];
 }
 
+template <class E>
 __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
                                                     const float* __restrict__ b, int R, int d, float* __restrict__ out) {
   const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -286,7 +289,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict_
   float acc = 0.0f;
   for (int o = lane * 8; o < d; o += 512) {
     float v[8], wv[8];
-    unpack8(*reinterpret_cast<const uint4*>(x + size_t(row) * d + o), v);
+    unpack8<E>(*reinterpret_cast<const uint4*>(x + size_t(row) * d + o), v);
     load8f(w + o, wv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += v[e] * wv[e];
@@ -301,67 +304,93 @@ __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t* __restrict_
 // row per workgroup instead, so its few rows spread over that many CUs rather than a quarter of them.
 inline int row_waves(int T) { return T < 2048 ? 1 : 4; }
 
-void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
-                     uint16_t* x_out, hipStream_t st) {
-  if (T <= 0) return;
+template <class E>
+void embed_ln_t(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
+                uint16_t* x_out, hipStream_t st) {
   const int rw = row_waves(T);
   dim3 grid((T + rw - 1) / rw), block(64 * rw);
   switch (d) {
-    case 512: hipLaunchKernelGGL(embed_ln_kernel<8>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
-    case 1024: hipLaunchKernelGGL(embed_ln_kernel<16>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
-    case 2048: hipLaunchKernelGGL(embed_ln_kernel<32>, grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 512: hipLaunchKernelGGL((embed_ln_kernel<E, 8>), grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 1024: hipLaunchKernelGGL((embed_ln_kernel<E, 16>), grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+    case 2048: hipLaunchKernelGGL((embed_ln_kernel<E, 32>), grid, block, 0, st, tok_emb, ids, w, eps, T, d, h_out, x_out); break;
+  }
+}
+
+void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
+                     uint16_t* x_out, hipStream_t st, int elem) {
+  if (T <= 0) return;
+  if (elem == ELEM_F16) embed_ln_t<F16>(tok_emb, ids, w, eps, T, d, h_out, x_out, st);
+  else embed_ln_t<Bf16>(tok_emb, ids, w, eps, T, d, h_out, x_out, st);
+}
+
+template <class E>
+void layernorm_t(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
+                 uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus, hipStream_t st) {
+  const int rw = row_waves(T);
+  dim3 grid((T + rw - 1) / rw), block(64 * rw);
+  switch (d) {
+    case 512:
+      hipLaunchKernelGGL((layernorm_kernel<E, 8>), grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+    case 1024:
+      hipLaunchKernelGGL((layernorm_kernel<E, 16>), grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
+    case 2048:
+      hipLaunchKernelGGL((layernorm_kernel<E, 32>), grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      break;
   }
 }
 
 void layernorm_launch(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
                       uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
-                      hipStream_t st) {
+                      hipStream_t st, int elem) {
   if (T <= 0) return;
+  if (elem == ELEM_F16) layernorm_t<F16>(x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus, st);
+  else layernorm_t<Bf16>(x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus, st);
+}
+
+template <class E>
+void splitk_resid_ln_t(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T, int d,
+                       uint16_t* y, hipStream_t st) {
   const int rw = row_waves(T);
   dim3 grid((T + rw - 1) / rw), block(64 * rw);
   switch (d) {
     case 512:
-      hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL((splitk_resid_ln_kernel<E, 8>), grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
     case 1024:
-      hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL((splitk_resid_ln_kernel<E, 16>), grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
     case 2048:
-      hipLaunchKernelGGL(layernorm_kernel<32>, grid, block, 0, st, x, rows, w, b, eps, T, d, y_bf16, y_f32, add_rowvec, seg, y_plus);
+      hipLaunchKernelGGL((splitk_resid_ln_kernel<E, 32>), grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
       break;
   }
 }
 
 void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T,
-                            int d, uint16_t* y, hipStream_t st) {
+                            int d, uint16_t* y, hipStream_t st, int elem) {
   if (T <= 0) return;
-  const int rw = row_waves(T);
-  dim3 grid((T + rw - 1) / rw), block(64 * rw);
-  switch (d) {
-    case 512:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<8>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
-      break;
-    case 1024:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<16>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
-      break;
-    case 2048:
-      hipLaunchKernelGGL(splitk_resid_ln_kernel<32>, grid, block, 0, st, ws, splits, bias, h, w, eps, T, d, y);
-      break;
-  }
+  if (elem == ELEM_F16) splitk_resid_ln_t<F16>(ws, splits, bias, h, w, eps, T, d, y, st);
+  else splitk_resid_ln_t<Bf16>(ws, splits, bias, h, w, eps, T, d, y, st);
 }
 
 void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
-                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st) {
+                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st, int elem) {
   const long long n = (long long)T * (d / 64) * 4;
   if (n <= 0) return;
-  hipLaunchKernelGGL(split_rope_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, T, d, pos, cos_t, sin_t,
-                     q, k, v, ldv);
+  const dim3 grid(unsigned((n + 255) / 256)), block(256);
+  if (elem == ELEM_F16)
+    hipLaunchKernelGGL(split_rope_kernel<F16>, grid, block, 0, st, qkv, T, d, pos, cos_t, sin_t, q, k, v, ldv);
+  else
+    hipLaunchKernelGGL(split_rope_kernel<Bf16>, grid, block, 0, st, qkv, T, d, pos, cos_t, sin_t, q, k, v, ldv);
 }
 
-void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st) {
+void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st, int elem) {
   const long long n = (long long)T * (I / 8);
   if (n <= 0) return;
-  hipLaunchKernelGGL(geglu_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, wi, T, I, act);
+  const dim3 grid(unsigned((n + 255) / 256)), block(256);
+  if (elem == ELEM_F16) hipLaunchKernelGGL(geglu_kernel<F16>, grid, block, 0, st, wi, T, I, act);
+  else hipLaunchKernelGGL(geglu_kernel<Bf16>, grid, block, 0, st, wi, T, I, act);
 }
 
 void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out, hipStream_t st) {
@@ -369,9 +398,11 @@ void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out
   hipLaunchKernelGGL(gather_f32_kernel, dim3(R), dim3(256), 0, st, x, rows, R, d, out);
 }
 
-void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st) {
+void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st,
+                   int elem) {
   if (R <= 0) return;
-  hipLaunchKernelGGL(rowdot_kernel, dim3((R + 3) / 4), dim3(256), 0, st, x, w, b, R, d, out);
+  if (elem == ELEM_F16) hipLaunchKernelGGL(rowdot_kernel<F16>, dim3((R + 3) / 4), dim3(256), 0, st, x, w, b, R, d, out);
+  else hipLaunchKernelGGL(rowdot_kernel<Bf16>, dim3((R + 3) / 4), dim3(256), 0, st, x, w, b, R, d, out);
 }
 
 }  // namespace s1

@@ -6,9 +6,10 @@
 // of one row with a single 16-byte LDS read.
 //
 // Tiling: a BM x BN x 64 block tile in 4 wavefronts; each wave owns a (BM/WM) x (BN/WN) sub-tile
-// computed with v_mfma_f32_32x32x16_bf16. Operands move global -> LDS directly
-// (global_load_lds_dwordx4, no registers), STAGES k-tiles deep, one barrier per k-tile; a
-// 16-byte-chunk XOR swizzle keeps the fragment reads free of bank conflicts.
+// computed with v_mfma_f32_32x32x16_bf16 (v_mfma_f32_32x32x16_f16 for f16 operands: the element
+// type E is a template parameter). Operands move global -> LDS directly (global_load_lds_dwordx4,
+// no registers), STAGES k-tiles deep, one barrier per k-tile; a 16-byte-chunk XOR swizzle keeps
+// the fragment reads free of bank conflicts.
 //
 // MFMA 32x32x16 lane layout (per operand, lane l, h = l / 32): the first operand supplies row
 // l % 32, k = 8h..8h+7; the second supplies column l % 32, k = 8h..8h+7; the 16 accumulators of
@@ -67,7 +68,7 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 // as one 8-byte (bf16) or 16-byte (f32) access after a packed conversion. !TR: D = A . W^T, a
 // lane holds one column and four consecutive rows per g; only the transposed v output of the
 // q|k|v epilogue ([H, 64, ldv], rows = tokens contiguous) wants that.
-template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0, int n0, int kt0, int NK, int split) {
   constexpr int NW = WM * WN;                // waves; each owns a TM x TN sub-tile
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -139,17 +140,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
     const int pstage = (it + STAGES - 1) % STAGES, pkt = kt0 + it + STAGES - 1;
     const char* sa = smem + (it % STAGES) * STAGE_BYTES;
     const char* sw = sa + A_BYTES;
-    bf16x8 af[2][FM], bw[2][FN];
+    typedef typename E::v8 v8;
+    v8 af[2][FM], bw[2][FN];
     auto frag = [&](int ks, int buf) {
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * TM + i * 32 + lr;
-        af[buf][i] = *reinterpret_cast<const bf16x8*>(sa + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
+        af[buf][i] = *reinterpret_cast<const v8*>(sa + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int row = wn * TN + j * 32 + lr;
-        bw[buf][j] = *reinterpret_cast<const bf16x8*>(sw + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
+        bw[buf][j] = *reinterpret_cast<const v8*>(sw + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
       }
     };
     frag(0, 0);
@@ -163,9 +165,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           if constexpr (TR)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+            acc[i][j] = E::mfma(bw[ks & 1][j], af[ks & 1][i], acc[i][j]);
           else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bw[ks & 1][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = E::mfma(af[ks & 1][i], bw[ks & 1][j], acc[i][j]);
         }
     }
   }
@@ -205,9 +207,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
             const f32x16& a1 = acc[mi][2 * p];
             const f32x16& a2 = acc[mi][2 * p + 1];
             *reinterpret_cast<uint2*>(col1 + rl * 2) =
-                make_uint2(pack2(a1[q4 * 4] + b1, a1[q4 * 4 + 1] + b1), pack2(a1[q4 * 4 + 2] + b1, a1[q4 * 4 + 3] + b1));
+                make_uint2(E::pack2(a1[q4 * 4] + b1, a1[q4 * 4 + 1] + b1), E::pack2(a1[q4 * 4 + 2] + b1, a1[q4 * 4 + 3] + b1));
             *reinterpret_cast<uint2*>(col2 + rl * 2) =
-                make_uint2(pack2(a2[q4 * 4] + b2, a2[q4 * 4 + 1] + b2), pack2(a2[q4 * 4 + 2] + b2, a2[q4 * 4 + 3] + b2));
+                make_uint2(E::pack2(a2[q4 * 4] + b2, a2[q4 * 4 + 1] + b2), E::pack2(a2[q4 * 4 + 2] + b2, a2[q4 * 4 + 3] + b2));
           }
       }
       __syncthreads();
@@ -242,7 +244,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
       float* out = part ? g.ws + size_t(split) * g.M * g.N : reinterpret_cast<float*>(g.C);
       const int ld = part ? g.N : g.ldc;
       constexpr int PF = BN * 4 + 16;
-      constexpr int NHF = BM * PF <= STAGES * STAGE_BYTES ? 1 : 2;
+      constexpr int NHF = BM * PF <= STAGES * STAGE_BYTES ? 1 : BM / 2 * PF <= STAGES * STAGE_BYTES ? 2 : 4;
       constexpr int HRF = BM / NHF;
       static_assert(HRF * PF <= STAGES * STAGE_BYTES && HRF % 32 == 0, "f32 staging must fit the stage buffers");
 #pragma unroll
@@ -295,8 +297,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
             const f32x16& x = acc[i][2 * p];
             const f32x16& gt = acc[i][2 * p + 1];
             *reinterpret_cast<uint2*>(crow + p * 32 + q * 8) =
-                make_uint2(pack2(gelu_erf(x[4 * q]) * gt[4 * q], gelu_erf(x[4 * q + 1]) * gt[4 * q + 1]),
-                           pack2(gelu_erf(x[4 * q + 2]) * gt[4 * q + 2], gelu_erf(x[4 * q + 3]) * gt[4 * q + 3]));
+                make_uint2(E::pack2(gelu_erf(x[4 * q]) * gt[4 * q], gelu_erf(x[4 * q + 1]) * gt[4 * q + 1]),
+                           E::pack2(gelu_erf(x[4 * q + 2]) * gt[4 * q + 2], gelu_erf(x[4 * q + 3]) * gt[4 * q + 3]));
           }
       }
     } else {
@@ -344,8 +346,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
                   }
                 }
                 char* o = stg + (rl0 + i * 32 - half * HR) * P + (c0 - n0 + i0) * 2;
-                *reinterpret_cast<uint2*>(o) = make_uint2(pack2(x1[0], x1[1]), pack2(x1[2], x1[3]));
-                *reinterpret_cast<uint2*>(o + 64) = make_uint2(pack2(x2[0], x2[1]), pack2(x2[2], x2[3]));
+                *reinterpret_cast<uint2*>(o) = make_uint2(E::pack2(x1[0], x1[1]), E::pack2(x1[2], x1[3]));
+                *reinterpret_cast<uint2*>(o + 64) = make_uint2(E::pack2(x2[0], x2[1]), E::pack2(x2[2], x2[3]));
               }
             }
           }
@@ -366,7 +368,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
                   else if (g.act == ACT_GELU) v[r] = gelu_erf(v[r]);
                 }
                 *reinterpret_cast<uint2*>(stg + (rl0 + i * 32 - half * HR) * P + (cl0 + j * 32 + q * 8) * 2) =
-                    make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+                    make_uint2(E::pack2(v[0], v[1]), E::pack2(v[2], v[3]));
               }
             }
         }
@@ -393,7 +395,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
   }
 }
 
-template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of BK * 2 bytes. The 16-byte chunk c
   // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
@@ -422,17 +424,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 
   if constexpr (EPI == EPI_ROPE) {
     if (n0 >= 2 * g.rope_d) {
-      gemm_tile<BM, BN, BK, STAGES, WM, WN, EPI, false>(g, smem, m0, n0, kt0, NK, split);
+      gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, false>(g, smem, m0, n0, kt0, NK, split);
       return;
     }
   }
-  gemm_tile<BM, BN, BK, STAGES, WM, WN, EPI, true>(g, smem, m0, n0, kt0, NK, split);
+  gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, true>(g, smem, m0, n0, kt0, NK, split);
 }
 
-template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
 void launch_t(const GemmArgs& g, hipStream_t st) {
   const int mt = (g.M + BM - 1) / BM, nt = g.N / BN;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, STAGES, WM, WN, EPI>), dim3(mt * nt, g.splits), dim3(WM * WN * 64), 0,
+  hipLaunchKernelGGL((gemm_kernel<E, BM, BN, BK, STAGES, WM, WN, EPI>), dim3(mt * nt, g.splits), dim3(WM * WN * 64), 0,
                      st, g);
 }
 
@@ -467,17 +469,24 @@ inline int tile_m_of(int M, int N) {
   }
 }
 
+template <class E, int EPI>
+void launch_te(const GemmArgs& g, hipStream_t st) {
+  switch (tile_cfg(g.M, g.N)) {
+    case TC_SMALL: launch_t<E, 64, 128, 64, 3, 2, 2, EPI>(g, st); break;
+    case TC_WIDE: launch_t<E, 192, 128, 64, 2, 2, 2, EPI>(g, st); break;
+    case TC_MID: launch_t<E, 64, 128, 64, 2, 2, 2, EPI>(g, st); break;
+  }
+}
+
 template <int EPI>
 void launch_e(const GemmArgs& g, hipStream_t st) {
-  switch (tile_cfg(g.M, g.N)) {
-    case TC_SMALL: launch_t<64, 128, 64, 3, 2, 2, EPI>(g, st); break;
-    case TC_WIDE: launch_t<192, 128, 64, 2, 2, 2, EPI>(g, st); break;
-    case TC_MID: launch_t<64, 128, 64, 2, 2, 2, EPI>(g, st); break;
-  }
+  if (g.elem == ELEM_F16) launch_te<F16, EPI>(g, st);
+  else launch_te<Bf16, EPI>(g, st);
 }
 
 // Sum of the split-K partials in split order, then the GEMM's epilogue. One thread per row and
 // column pair (c, c + 32) of a 64-column group, the pair the GeGLU and RoPE epilogues combine.
+template <class E>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   const int half = g.N / 2;
@@ -493,7 +502,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
   }
   if (g.epi == EPI_GEGLU) {
     uint16_t* C = reinterpret_cast<uint16_t*>(g.C);
-    C[size_t(row) * g.ldc + p] = f2bf(gelu_erf(x1) * x2);
+    C[size_t(row) * g.ldc + p] = E::bits(gelu_erf(x1) * x2);
     return;
   }
   if (g.epi == EPI_ROPE) {
@@ -513,8 +522,8 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
     }
     if (part == 2) {  // v transposed, [H, 64, ldv]
       uint16_t* o = g.rope_v + (size_t(head) * 64 + i) * g.rope_ldv + row;
-      o[0] = f2bf(x1);
-      o[size_t(32) * g.rope_ldv] = f2bf(x2);
+      o[0] = E::bits(x1);
+      o[size_t(32) * g.rope_ldv] = E::bits(x2);
       if (row == g.M - 1)  // zeros up to the next multiple of 8 tokens, as the GEMM's own epilogue
         for (int t = 1; row + t < (g.M + 7) / 8 * 8; ++t) {
           o[t] = 0;
@@ -523,8 +532,8 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
       return;
     }
     uint16_t* o = (part == 0 ? g.rope_q : g.rope_k) + (size_t(head) * g.rope_T + row) * 64;
-    o[i] = f2bf(x1);
-    o[i + 32] = f2bf(x2);
+    o[i] = E::bits(x1);
+    o[i + 32] = E::bits(x2);
     return;
   }
   const float b1 = g.bias ? g.bias[c1] : 0.0f, b2 = g.bias ? g.bias[c2] : 0.0f;
@@ -549,8 +558,8 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
     x2 = gelu_erf(x2);
   }
   uint16_t* C = reinterpret_cast<uint16_t*>(g.C) + size_t(row) * g.ldc;
-  C[c1] = f2bf(x1);
-  C[c2] = f2bf(x2);
+  C[c1] = E::bits(x1);
+  C[c2] = E::bits(x2);
 }
 
 }  // namespace
@@ -603,7 +612,9 @@ void gemm_launch(const GemmArgs& g, hipStream_t st) {
   if (g.splits > 1) {
     gemm_launch_partials(g, st);  // partials only: the kernel returns before its epilogue
     const long long n = (long long)g.M * (g.N / 2);
-    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, g);
+    const dim3 grid(unsigned((n + 255) / 256)), block(256);
+    if (g.elem == ELEM_F16) hipLaunchKernelGGL(splitk_epilogue_kernel<F16>, grid, block, 0, st, g);
+    else hipLaunchKernelGGL(splitk_epilogue_kernel<Bf16>, grid, block, 0, st, g);
     return;
   }
   switch (g.epi) {

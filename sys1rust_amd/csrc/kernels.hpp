@@ -7,6 +7,10 @@
 
 namespace s1 {
 
+// The 16-bit type of weights and activations (every "bf16" buffer below holds this type): bf16
+// by default, f16 with the model setting dtype=f16.
+enum Elem { ELEM_BF16 = 0, ELEM_F16 = 1 };
+
 enum GemmEpi { EPI_BF16 = 0, EPI_RESID = 1, EPI_GEGLU = 2, EPI_F32 = 3, EPI_ROPE = 4 };
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
 
@@ -19,6 +23,7 @@ struct GemmArgs {
   int lda = 0, ldw = 0, ldc = 0;
   int epi = EPI_BF16;
   int act = ACT_NONE;
+  int elem = ELEM_BF16;
   // Split-K: `splits` workgroups share each output tile, each over a contiguous k-range, and
   // write f32 partials [splits, M, N] to `ws`; a second kernel sums them in split order and runs
   // the epilogue. splits = 1 runs the epilogue in the GEMM and needs no workspace.
@@ -86,6 +91,7 @@ struct AttnArgs {
   // key), or 32: then key_waves (4 or 8) waves split each tile's keys.
   int tile_q = 256;
   int key_waves = 4;
+  int elem = ELEM_BF16;
 };
 void attn_launch(const AttnArgs& a, hipStream_t st);
 // Queries per work tile the attention kernel takes: 128 on local layers; on global layers 256 or
@@ -99,34 +105,35 @@ int attn_row_step(int len, int qb);
 
 // h[t] = LN(tok_emb[ids[t]]) (no bias), written as f32 and as bf16.
 void embed_ln_launch(const uint16_t* tok_emb, const int* ids, const float* w, float eps, int T, int d, float* h_out,
-                     uint16_t* x_out, hipStream_t st);
+                     uint16_t* x_out, hipStream_t st, int elem = ELEM_BF16);
 
 // y = LN(x) (optional bias) over rows of d, x f32; y bf16 and/or f32 (null to skip). With
 // `rows` the input row of output row t is rows[t]. With `add_rowvec`, the f32 output also gets
 // add_rowvec[seg[t]] (the type embedding of the row's question), used to start the head stream.
 void layernorm_launch(const float* x, const int* rows, const float* w, const float* b, float eps, int T, int d,
                       uint16_t* y_bf16, float* y_f32, const float* add_rowvec, const int* seg, float* y_plus,
-                      hipStream_t st);
+                      hipStream_t st, int elem = ELEM_BF16);
 
 // The end of a split-K residual GEMM and the LayerNorm after it, one wave per row:
 // h[t] += (sum over s of ws[s, t] in split order) + bias, then y[t] = LN(h[t]) (weight w, no
 // bias) in bf16. Bit for bit the GEMM's own split-K epilogue followed by layernorm_launch.
 // ws is [splits, T, d] f32, h is [T, d] f32.
 void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, float* h, const float* w, float eps, int T,
-                            int d, uint16_t* y, hipStream_t st);
+                            int d, uint16_t* y, hipStream_t st, int elem = ELEM_BF16);
 
 // Plain split (+ RoPE when cos/sin are given): qkv [T, 3d] bf16 -> q, k [H, T, 64] and v
 // transposed [H, 64, ldv] (ldv >= T), bf16.
 void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
-                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st);
+                       uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st, int elem = ELEM_BF16);
 
 // act[t, i] = gelu(wi[t, i]) * wi[t, I + i] for the un-interleaved Wi product.
-void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st);
+void geglu_launch(const uint16_t* wi, int T, int I, uint16_t* act, hipStream_t st, int elem = ELEM_BF16);
 
 // Gather rows: out[r] = x[rows[r]] for f32 rows of d.
 void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out, hipStream_t st);
 
 // logits[r] = dot(x[r], w) + b, x bf16 [R, d], w f32 [d].
-void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st);
+void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st,
+                   int elem = ELEM_BF16);
 
 }  // namespace s1

@@ -60,6 +60,11 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "fusegeglu") s.fusegeglu = flag();
     else if (key == "fuseln") s.fuseln = flag();
     else if (key == "graphs") s.graphs = flag();
+    else if (key == "dtype") {
+      if (val == "bf16") s.f16 = false;
+      else if (val == "f16") s.f16 = true;
+      else bad("dtype must be bf16 or f16");
+    }
     else if (key == "parallel_load") flag();  // read by the runtime (backend.rs:44-69); checked here too
     else if (key == "pad") {
       if (!has_val) bad("needs a value (`key=value`)");
@@ -110,6 +115,7 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
     : device(dev) {
   cfg = parse_model_config(enc_json, agent_json);
   set = Settings::parse(settings);
+  elem = set.f16 ? ELEM_F16 : ELEM_BF16;
   if (cfg.head_dim() != 64)
     fail(kConfig, "the HIP kernels need a head dim of 64; this encoder has " + std::to_string(cfg.head_dim()));
   if (cfg.d != 512 && cfg.d != 1024 && cfg.d != 2048)
@@ -262,11 +268,14 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
     }
     const size_t n = size_t(tv.numel());
     hb.resize(n);
-    if (tv.dtype == DType::BF16) {
+    // The tensor's bits when it is stored in the model's 16-bit type, else rounded from f32 (every
+    // bf16 and f16 value is exact in f32, so a tensor is rounded once).
+    const DType want = set.f16 ? DType::F16 : DType::BF16;
+    if (tv.dtype == want) {
       std::memcpy(hb.data(), tv.data, n * 2);
     } else {
       std::vector<float> f = st.to_f32(it.name, it.shape);
-      for (size_t e = 0; e < n; ++e) hb[e] = f32_to_bf16(f[e]);
+      for (size_t e = 0; e < n; ++e) hb[e] = set.f16 ? f32_to_f16(f[e]) : f32_to_bf16(f[e]);
     }
     if (it.perm == 1) {
       // Wi [2I, d] -> rows interleaved in blocks of 32: (x rows 32j.., gate rows I + 32j..).
@@ -282,7 +291,7 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
   }
 
   char nb[64];
-  std::snprintf(nb, sizeof nb, "hip(gfx950,bf16)");
+  std::snprintf(nb, sizeof nb, "hip(gfx950,%s)", set.f16 ? "f16" : "bf16");
   name = nb;
   kernels = "mfma";
   if (set.fuserope) kernels += ",fuserope";
@@ -574,9 +583,10 @@ void Model::collect_stats() {
 
 namespace {
 
-GemmArgs gemm_args(float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
+GemmArgs gemm_args(int elem, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
                    const float* bias, int M, int N, int epi, int act = ACT_NONE, bool reduce_folded = false) {
   GemmArgs g;
+  g.elem = elem;
   g.splits = gemm_plan(M, N, K, reduce_folded).splits;
   g.ws = ws;
   g.A = A;
@@ -595,9 +605,9 @@ GemmArgs gemm_args(float* ws, const uint16_t* A, int lda, const uint16_t* W, int
   return g;
 }
 
-void gemm(hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
+void gemm(int elem, hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
           const float* bias, int M, int N, int epi, int act = ACT_NONE) {
-  gemm_launch(gemm_args(ws, A, lda, W, K, C, ldc, bias, M, N, epi, act), st);
+  gemm_launch(gemm_args(elem, ws, A, lda, W, K, C, ldc, bias, M, N, epi, act), st);
 }
 
 }  // namespace
@@ -611,7 +621,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
   const AttnTile* ltiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_ltiles);
 
   // h = LN(tok_emb[ids]) (lib.rs:1534-1551); x = h for layer 0, which has no attn_norm.
-  op("embed_ln", [&] { embed_ln_launch(tok_emb, ids, emb_norm, eps, T, d, a.h, a.x, stream); });
+  op("embed_ln", [&] { embed_ln_launch(tok_emb, ids, emb_norm, eps, T, d, a.h, a.x, stream, elem); });
   // A residual GEMM that splits K hands its partials to the kernel of the LayerNorm after it,
   // which adds them into h and writes x = LN(h); x_ready marks an attn_norm done that way.
   bool x_ready = false;
@@ -620,11 +630,12 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
     const int tw = L.local ? 1 : 0;
     if (L.attn_norm && !x_ready)
       op("attn_norm", [&] {
-        layernorm_launch(a.h, nullptr, L.attn_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+        layernorm_launch(a.h, nullptr, L.attn_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
     if (set.fuserope) {
       op("wqkv_rope", [&] {
         GemmArgs g;
+        g.elem = elem;
         g.A = a.x;
         g.W = L.wqkv;
         g.M = T;
@@ -648,11 +659,12 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
         gemm_launch(g, stream);
       });
     } else {
-      op("wqkv", [&] { gemm(stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
-      op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, vt_ld(T), stream); });
+      op("wqkv", [&] { gemm(elem, stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
+      op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, vt_ld(T), stream, elem); });
     }
     op(L.local ? "attn_local" : "attn_global", [&] {
       AttnArgs at;
+      at.elem = elem;
       at.q = a.q;
       at.k = a.k;
       at.v = a.v;
@@ -673,28 +685,28 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
     // h = h + att . Wo^T (lib.rs:1666), x = mlp_norm(h) (lib.rs:1669)
     // Wo and Wo2 plan their split as finished by the LayerNorm after them (structurally, so the
     // fuseln=0 path splits the same way and stays bit-identical).
-    const GemmArgs gwo = gemm_args(a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, true);
+    const GemmArgs gwo = gemm_args(elem, a.ws, a.att, d, L.wo, d, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, true);
     if (set.fuseln && gwo.splits > 1) {
       op("wo", [&] { gemm_launch_partials(gwo, stream); });
-      op("mlp_norm", [&] { splitk_resid_ln_launch(a.ws, gwo.splits, nullptr, a.h, L.mlp_norm, eps, T, d, a.x, stream); });
+      op("mlp_norm", [&] { splitk_resid_ln_launch(a.ws, gwo.splits, nullptr, a.h, L.mlp_norm, eps, T, d, a.x, stream, elem); });
     } else {
       op("wo", [&] { gemm_launch(gwo, stream); });
       op("mlp_norm", [&] {
-        layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+        layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
     }
     if (set.fusegeglu) {
-      op("wi_geglu", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
+      op("wi_geglu", [&] { gemm(elem, stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
     } else {
-      op("wi", [&] { gemm(stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
-      op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream); });
+      op("wi", [&] { gemm(elem, stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
+      op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream, elem); });
     }
     // h = h + act . Wo2^T (lib.rs:1675), and the next layer's x = attn_norm(h) (lib.rs:1592-1595)
     const float* next_norm = l + 1 < cfg.layers ? layers[l + 1].attn_norm : nullptr;
-    const GemmArgs gwo2 = gemm_args(a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, next_norm != nullptr);
+    const GemmArgs gwo2 = gemm_args(elem, a.ws, a.act, I, L.wo2, I, a.h, d, nullptr, T, d, EPI_RESID, ACT_NONE, next_norm != nullptr);
     if (set.fuseln && gwo2.splits > 1 && next_norm) {
       op("wo2", [&] { gemm_launch_partials(gwo2, stream); });
-      op("attn_norm", [&] { splitk_resid_ln_launch(a.ws, gwo2.splits, nullptr, a.h, next_norm, eps, T, d, a.x, stream); });
+      op("attn_norm", [&] { splitk_resid_ln_launch(a.ws, gwo2.splits, nullptr, a.h, next_norm, eps, T, d, a.x, stream, elem); });
       x_ready = true;
     } else {
       op("wo2", [&] { gemm_launch(gwo2, stream); });
@@ -772,7 +784,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
   run_encoder(p, a);
   // final_norm (lib.rs:1689), then h + type_emb[qtype] per row (lib.rs:1702-1709) in one pass.
   op("final_norm", [&] {
-    layernorm_launch(a.h, nullptr, final_norm, nullptr, eps, T, d, nullptr, nullptr, type_emb, seg, a.hh, stream);
+    layernorm_launch(a.h, nullptr, final_norm, nullptr, eps, T, d, nullptr, nullptr, type_emb, seg, a.hh, stream, elem);
   });
   const AttnTile* tiles = reinterpret_cast<const AttnTile*>(dmeta + p.off_tiles);
   const float hscale = 1.0f / std::sqrt(float(d / cfg.head_nheads()));  // head_scale (lib.rs:576-578)
@@ -782,11 +794,12 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
     const bool pruned = set.headprune && j + 1 == nh;
     // x = norm1(h); qkv = x . in_proj^T + b; split heads (lib.rs:1726-1741)
     op("head_norm1", [&] {
-      layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+      layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
     });
     // in_proj + bias with the head split fused in its epilogue (no rotation in the head)
     op("head_in_proj", [&] {
       GemmArgs g;
+      g.elem = elem;
       g.A = a.x;
       g.W = Hw.in_w;
       g.bias = Hw.in_b;
@@ -810,6 +823,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
     if (!pruned) {
       op("head_attn", [&] {
         AttnArgs at;
+        at.elem = elem;
         at.q = a.q;
         at.k = a.k;
         at.v = a.v;
@@ -825,18 +839,19 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.scale = hscale;
         attn_launch(at, stream);
       });
-      op("head_out_proj", [&] { gemm(stream, a.ws, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(elem, stream, a.ws, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
       op("head_norm2", [&] {
-        layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream);
+        layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
-      op("head_linear1", [&] { gemm(stream, a.ws, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(stream, a.ws, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(elem, stream, a.ws, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(elem, stream, a.ws, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
     } else {
       // headprune (lib.rs:1728-1748): every token supplies k and v; queries, out_proj, norm2 and
       // the FFN run at rows {0, markers} only.
       const int* picked = dmeta + p.off_picked;
       op("head_attn", [&] {
         AttnArgs at;
+        at.elem = elem;
         at.q = a.q;
         at.k = a.k;
         at.v = a.v;
@@ -857,12 +872,12 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         attn_launch(at, stream);
       });
       op("head_pick", [&] { gather_f32_launch(a.hh, picked, P, d, a.hp, stream); });
-      op("head_out_proj", [&] { gemm(stream, a.ws, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(elem, stream, a.ws, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
       op("head_norm2", [&] {
-        layernorm_launch(a.hp, nullptr, Hw.n2w, Hw.n2b, 1e-5f, P, d, a.xp, nullptr, nullptr, nullptr, nullptr, stream);
+        layernorm_launch(a.hp, nullptr, Hw.n2w, Hw.n2b, 1e-5f, P, d, a.xp, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
-      op("head_linear1", [&] { gemm(stream, a.ws, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(stream, a.ws, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(elem, stream, a.ws, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(elem, stream, a.ws, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
     }
   }
   // score (lib.rs:1768-1800): LN_b at the marker rows, scorer1 + GELU, scorer3; pooled row 0.
@@ -871,10 +886,10 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
   const int* prows = dmeta + p.off_pooled;
   if (R > 0) {
     op("scorer_norm", [&] {
-      layernorm_launch(src, srows, sc0_w, sc0_b, 1e-5f, R, d, a.sx, nullptr, nullptr, nullptr, nullptr, stream);
+      layernorm_launch(src, srows, sc0_w, sc0_b, 1e-5f, R, d, a.sx, nullptr, nullptr, nullptr, nullptr, stream, elem);
     });
-    op("scorer1", [&] { gemm(stream, a.ws, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
-    op("scorer3", [&] { rowdot_launch(a.s1, sc3_w, sc3_b, R, S, a.logits, stream); });
+    op("scorer1", [&] { gemm(elem, stream, a.ws, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
+    op("scorer3", [&] { rowdot_launch(a.s1, sc3_w, sc3_b, R, S, a.logits, stream, elem); });
   }
   op("pooled", [&] { gather_f32_launch(src, prows, n, d, a.pooled, stream); });
 }
@@ -919,7 +934,7 @@ void Model::encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden) {
     run_encoder(p, a);
     op("final_norm", [&] {
       layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, nullptr, nullptr,
-                       nullptr, stream);
+                       nullptr, stream, elem);
     });
   });
   std::vector<float> packed(size_t(T) * d);

@@ -24,6 +24,7 @@ struct Settings {
   bool fusegeglu = true;   // GeGLU fused into the Wi GEMM epilogue (Wi rows interleaved at load)
   bool fuseln = true;      // a split-K Wo / Wo2 finishes in the kernel of the LayerNorm after it
   bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
+  bool f16 = false;        // dtype=f16: weights and activations in f16 (the checkpoint's type), not bf16
   size_t pad = 1;          // padded_len multiple
   std::vector<size_t> buckets;
   static Settings parse(const std::string& spec);
@@ -82,6 +83,7 @@ struct Plan {
 struct Model {
   ModelConfig cfg;
   Settings set;
+  int elem = ELEM_BF16;  // 16-bit type of weights and activations (set.f16)
   int device = 0;
   int scorer_width = 0;
   hipStream_t stream = nullptr;

@@ -145,6 +145,49 @@ def test_f32_and_f16_checkpoints_load_like_bf16(small_model, dtype):
     m1.close()
 
 
+def test_f16_matches_oracle_closer_than_bf16(small_model):
+    """dtype=f16 runs every kernel on f16 operands (three more mantissa bits than bf16, the
+    checkpoints' own type). It passes the gates, and its distance to the f32 oracle is well under
+    the bf16 path's: a kernel left on bf16 conversions, or on the bf16 MFMA, would not be."""
+    cfg, agent, st, b, z = small_model
+    say("f16: create")
+    m16 = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f16")
+    mbf = HipBackend(st, json.dumps(cfg), json.dumps(agent))
+    assert m16.name() == "hip(gfx950,f16)"
+    o = O.Oracle(st, cfg, agent)
+    ref = o.encoder_hidden(b)
+    r16 = hidden_rel(m16.encoder_hidden(b).reshape(b.n, b.len, -1), ref, b)
+    rbf = hidden_rel(mbf.encoder_hidden(b).reshape(b.n, b.len, -1), ref, b)
+    say(f"f16: hidden rel {r16:.3e} (bf16 {rbf:.3e})")
+    assert r16 <= HIDDEN_REL_GATE and r16 <= 0.2 * rbf, (r16, rbf)
+    lg_ref, pl_ref = o.forward(b, ref)
+    for name in ("fuserope=0,fusegeglu=0,fuseln=0,headprune=0", ""):
+        mm = m16 if not name else HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f16," + name)
+        out = mm.forward(b)
+        check_answers(out.logits, lg_ref, b, f"f16 {name or 'default'}")
+        p16 = float(np.linalg.norm(out.pooled - pl_ref) / np.linalg.norm(pl_ref))
+        pbf = float(np.linalg.norm(mbf.forward(b).pooled - pl_ref) / np.linalg.norm(pl_ref))
+        say(f"f16 {name or 'default'}: pooled rel {p16:.3e} (bf16 {pbf:.3e})")
+        assert p16 <= 0.2 * pbf, (name, p16, pbf)
+    m16.close()
+    mbf.close()
+
+
+def test_f16_model_keeps_f16_checkpoint_bits(small_model):
+    """With dtype=f16 an F16 checkpoint's tensors are used as stored; the bf16 checkpoint's are
+    rounded to f16 on load (round to nearest even, as numpy's astype(float16) that wrote the F16
+    file), so both give the same weights and the same bits out."""
+    cfg, agent, st, b, z = small_model
+    say("f16 checkpoint with dtype=f16")
+    a = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f16")
+    c = HipBackend(_reencode(st, "F16"), json.dumps(cfg), json.dumps(agent), settings="dtype=f16")
+    oa, oc = a.forward(b), c.forward(b)
+    assert np.array_equal(oa.logits, oc.logits) and np.array_equal(oa.pooled, oc.pooled)
+    assert np.array_equal(a.encoder_hidden(b), c.encoder_hidden(b))
+    a.close()
+    c.close()
+
+
 def test_graph_replays_match_eager_runs(small_model):
     """Repeated shapes replay a captured HIP graph: every replay, interleaved with other shapes
     and with eager work, gives the eager path's bits."""
@@ -208,6 +251,27 @@ def test_modernbert_large_ten_questions(large):
     # other GEMM splits, so bf16 rounding differs in the last bits; compare at the answer gates.)
     alone = m.forward(sub)
     check_answers(alone.logits, lg, sub, "state512_10q rows alone")
+
+
+@pytest.mark.parametrize("name", ["state128_1q", "state512_1q", "state512_10q"])
+def test_modernbert_large_f16(large, name):
+    """The f16 path at the full shape: gates against the oracle, and closer than bf16."""
+    m, o = large
+    st = synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
+    m16 = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="dtype=f16")
+    b = workload(name, seed=1)
+    rows = [0] if b.n == 1 else [0, 4, 7]
+    sub = b.rows(rows)
+    say(f"f16 {name}: T={b.total_tokens()}")
+    ref = o.encoder_hidden(sub)
+    r16 = hidden_rel(m16.encoder_hidden(b).reshape(b.n, b.len, -1)[rows], ref, sub)
+    rbf = hidden_rel(m.encoder_hidden(b).reshape(b.n, b.len, -1)[rows], ref, sub)
+    say(f"f16 {name}: hidden rel {r16:.3e} (bf16 {rbf:.3e})")
+    assert r16 <= HIDDEN_REL_GATE and r16 <= 0.2 * rbf, (r16, rbf)
+    lg_ref, _ = o.forward(sub, ref)
+    lg = m16.forward(b).logits.reshape(b.n, b.kmax)[rows].reshape(-1)
+    check_answers(lg, lg_ref, sub, f"f16 {name}")
+    m16.close()
 
 
 def test_fused_split_k_layernorm_bit_exact(large):

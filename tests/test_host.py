@@ -53,11 +53,27 @@ def small_ckpt():
     ("pad=x", "is not a whole number"),
     ("buckets", "needs a value"),
     ("headprune,nax=all", "unknown setting `nax`"),
+    ("dtype=fp8", "dtype must be bf16 or f16"),
+    ("dtype", "dtype must be bf16 or f16"),
 ])
 def test_settings_are_strict(small_ckpt, spec, needle):
     with pytest.raises(S1Error) as e:
         HipBackend(small_ckpt, SMALL, json.dumps(AGENT), settings=spec)
     assert e.value.kind == "Config" and needle in str(e.value), str(e.value)
+
+
+@pytest.mark.parametrize("spec", ["dtype=f16", "dtype=bf16", "dtype=f16,dtype=bf16"])
+def test_dtype_setting_is_accepted(small_ckpt, spec):
+    """A valid dtype passes the settings check: without a GPU the create fails later, at the
+    device (a Backend error), never as a Config error."""
+    try:
+        m = HipBackend(small_ckpt, SMALL, json.dumps(AGENT), settings=spec)
+    except S1Error as e:
+        assert e.kind != "Config", str(e)
+        return
+    want = "f16" if spec.endswith("f16") else "bf16"
+    assert m.name() == f"hip(gfx950,{want})"
+    m.close()
 
 
 @pytest.mark.parametrize("mutate,needle", [
