@@ -275,6 +275,17 @@ def main() -> int:
                       f"(encoder, head, scorer, decode), scaled by {b.n}; rows are independent",
         }
         print(f"[bench] cpu baseline {cpu['value']} ms/request on {threads} threads", file=sys.stderr, flush=True)
+        # The same sample on 4 BLAS threads, the thread count of the published upstream fp32 CPU
+        # figures (M5 CPU, 4 threads).
+        if threads > 4:
+            from threadpoolctl import threadpool_limits
+
+            with threadpool_limits(limits=4, user_api="blas"):
+                t = time.perf_counter()
+                lg, _ = o.forward(sub)
+                decode_answers(lg, sub.kmax, sub.marker_count, sub.qtype)
+                cpu["value_4_threads"] = round((time.perf_counter() - t) * 1e3 / len(rows) * b.n, 1)
+            print(f"[bench] cpu baseline {cpu['value_4_threads']} ms/request on 4 threads", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,

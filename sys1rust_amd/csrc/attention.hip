@@ -226,7 +226,7 @@ void attn_kernel(AttnArgs a) {
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
       }
       // Online softmax in base 2: p = 2^(s * sl2 - m). sl2 > 0, so the raw max scales.
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = half_max(mx);
       const float mn = fmaxf(m, mx * sl2);
       const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is exp2(-inf) = 0
       const float alpha = __builtin_amdgcn_exp2f(m - ms);
@@ -276,7 +276,7 @@ void attn_kernel(AttnArgs a) {
   }
 
   if (!wave_active) return;
-  const float lt = l + __shfl_xor(l, 32, 64);
+  const float lt = half_sum(l);
   if (!qvalid) return;
   const float inv = 1.0f / lt;
   uint16_t* orow = a.out + size_t(qi) * a.ldo + head * 64;
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   }
   // Every real query sees itself, so the row maximum is finite.
   const float sl2 = a.scale * 1.4426950408889634f;
-  const float ms = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+  const float ms = half_max(mx) * sl2;
   float psum = 0.0f;
   f32x16 o[2];
 #pragma unroll
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       }
     }
   }
-  const float lt = psum + __shfl_xor(psum, 32, 64);
+  const float lt = half_sum(psum);
   if (!qvalid) return;
   const float inv = 1.0f / lt;
   uint16_t* orow = a.out + size_t(qi) * a.ldo + head * 64;
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = half_max(mx);
     const float mn = fmaxf(m, mx * sl2);
     const float ms = mn == NEG_INF ? 0.0f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ms);
@@ -610,7 +610,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 
   // Merge: wave w leaves (m, l, o) per lane in LDS; wave 0 combines them. A wave that visited no
   // chunk has m = -inf and contributes 0.
-  const float lw = l + __shfl_xor(l, 32, 64);
+  const float lw = half_sum(l);
   __syncthreads();  // every wave is done with its chunk buffers
   float* mt = reinterpret_cast<float*>(smem);  // [KW][64] m, [KW][64] l, [KW][32][64] o
   float* lt = mt + KW * 64;

@@ -83,16 +83,58 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
   return v;
 }
 
-// Sum / max over the 64 lanes of a wavefront.
+// Cross-lane steps on the VALU: DPP moves within a row of 16 lanes (quad_perm for lane ^ 1 and
+// lane ^ 2, row_half_mirror and row_mirror to join 4- and 8-lane groups), and gfx950's
+// v_permlane16_swap / v_permlane32_swap between rows and between the wave's halves. A
+// __shfl_xor is a ds_bpermute through the LDS pipe: a reduction of 6 of them in a chain waits on
+// 6 LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// x and the value of lane l ^ 16 (within each half), as a pair (own row's first).
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// The value of lane l % 32 and of lane l % 32 + 32, in every lane.
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// v(l) + v(l ^ 32) and max(v(l), v(l ^ 32)), the same bits in both lanes.
+__device__ __forceinline__ float half_sum(float v) {
+  float a, b;
+  swap32(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float half_max(float v) {
+  float a, b;
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum / max over the 64 lanes of a wavefront; every lane gets the same bits (each step combines
+// the same two partial results in the same order in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp<0xb1>(v);   // quad_perm(1, 0, 3, 2): lane ^ 1
+  v += dpp<0x4e>(v);   // quad_perm(2, 3, 0, 1): lane ^ 2
+  v += dpp<0x141>(v);  // row_half_mirror: the other quad of the 8
+  v += dpp<0x140>(v);  // row_mirror: the other 8 of the 16
+  float a, b;
+  swap16(v, a, b);
+  return half_sum(a + b);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp<0xb1>(v));
+  v = fmaxf(v, dpp<0x4e>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  float a, b;
+  swap16(v, a, b);
+  return half_max(fmaxf(a, b));
 }
 
 // GELU with the error function, 0.5 x (1 + erf(x / sqrt 2)), erf by Abramowitz & Stegun 7.1.26:

@@ -28,14 +28,15 @@ __device__ __forceinline__ void ln_stats(const float* v, int d, float eps, float
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < PL; ++i) s += v[i];
-  mean = wave_sum(s) / float(d);
+  // d = 64 PL, a power of two: the product by 1 / d is the quotient, exactly.
+  mean = wave_sum(s) * (1.0f / float(PL * 64));
   float q = 0.0f;
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const float c = v[i] - mean;
     q += c * c;
   }
-  const float var = wave_sum(q) / float(d);
+  const float var = wave_sum(q) * (1.0f / float(PL * 64));
   rstd = 1.0f / sqrtf(var + eps);
 }
 
