@@ -477,11 +477,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 // dependent chunks. Each wave stages its own chunks in a private 16 KiB of LDS (K rows and V^T
 // in the layouts attn_kernel uses), so the chunk loop has no barriers; the next chunk is loaded
 // into registers during this one's math and stored after it (a wave's LDS accesses run in
-// order), which keeps the workgroup at 64 KiB: two fit a CU.
+// order), which keeps 4 waves at 64 KiB (two workgroups per CU) and 8 at 128 KiB.
 template <class E, int KW>
 __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_ksplit_kernel(AttnArgs a) {
   typedef typename E::v8 v8;
-  constexpr int REG = KC * 64;  // bf16 elements of one 8 KiB K or V^T chunk
+  constexpr int REG = KC * 64;  // 16-bit elements of one 8 KiB K or V^T chunk
   // [wave] x (K | V^T); after the chunk loop the same memory holds the merge tables.
   __shared__ __attribute__((aligned(1024))) uint16_t smem[KW * 2 * REG];
 
