@@ -69,6 +69,23 @@ def test_state8192_single_question(big):
     assert pr <= HIDDEN_REL_GATE
 
 
+def test_state8192_f16(big):
+    """The f16 path on the longest row: gates against the checker, and closer than bf16."""
+    m, o, t = big
+    b = workload("state8192_1q", seed=1)
+    st = synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
+    m16 = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="dtype=f16")
+    say(f"state8192_1q f16: T={b.total_tokens()}")
+    ref = t.encoder_hidden(b)
+    r16 = hidden_rel(m16.encoder_hidden(b).reshape(b.n, b.len, -1), ref, b)
+    rbf = hidden_rel(m.encoder_hidden(b).reshape(b.n, b.len, -1), ref, b)
+    say(f"state8192_1q f16: hidden rel {r16:.3e} (bf16 {rbf:.3e})")
+    assert r16 <= HIDDEN_REL_GATE and r16 <= 0.2 * rbf, (r16, rbf)
+    lg_ref, _ = t.forward(b, ref)
+    check_answers(m16.forward(b).logits, lg_ref, b, "state8192_1q f16")
+    m16.close()
+
+
 def test_sweep64_packed_batch(big):
     m, _, t = big
     b = workload("sweep64", seed=1)
