@@ -31,7 +31,10 @@ COMMON = [
     "-I", str(ROOT / "include"),
 ]
 
-SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "model.cpp", "api.cpp", "safetensors.cpp", "synth.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "model.cpp", "api.cpp", "safetensors.cpp", "synth.cpp",
+           "blaslt.cpp"]
+# hipBLASLt for the plain residual GEMMs (csrc/blaslt.cpp), from the ROCm install.
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def _compile(src: str) -> Path:
@@ -54,7 +57,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", str(tmp), *map(str, objs)]
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", str(tmp), *map(str, objs), *LIBS]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

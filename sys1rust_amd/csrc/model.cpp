@@ -5,6 +5,7 @@
 // tokens only, and attention reads each row's token range directly instead of expanding to
 // [n, len].
 #include "model.hpp"
+#include "blaslt.hpp"
 
 #include <chrono>
 #include <cstdio>
@@ -60,6 +61,7 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "fusegeglu") s.fusegeglu = flag();
     else if (key == "fuseln") s.fuseln = flag();
     else if (key == "graphs") s.graphs = flag();
+    else if (key == "blaslt") s.blaslt = flag();
     else if (key == "dtype") {
       if (val == "bf16") s.f16 = false;
       else if (val == "f16") s.f16 = true;
@@ -299,6 +301,7 @@ Model::Model(const uint8_t* st_bytes, size_t st_len, const std::string& what, co
   if (set.fusegeglu) kernels += ",fusegeglu";
   if (set.fuseln) kernels += ",fuseln";
   if (set.headprune) kernels += ",headprune";
+  if (set.blaslt) kernels += ",blaslt";
 }
 
 Model::~Model() {
@@ -605,9 +608,16 @@ GemmArgs gemm_args(int elem, float* ws, const uint16_t* A, int lda, const uint16
   return g;
 }
 
-void gemm(int elem, hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C, int ldc,
-          const float* bias, int M, int N, int epi, int act = ACT_NONE) {
-  gemm_launch(gemm_args(elem, ws, A, lda, W, K, C, ldc, bias, M, N, epi, act), st);
+// A residual GEMM without split from LT_MIN_M rows goes to hipBLASLt when `lt` (setting blaslt);
+// everything else, and a shape hipBLASLt has no workspace-free algorithm for, to gemm_launch.
+void launch_gemm(const GemmArgs& g, hipStream_t st, bool lt) {
+  if (lt && g.epi == EPI_RESID && g.splits == 1 && g.M >= LT_MIN_M && lt_resid_gemm(g, st)) return;
+  gemm_launch(g, st);
+}
+
+void gemm(int elem, bool lt, hipStream_t st, float* ws, const uint16_t* A, int lda, const uint16_t* W, int K, void* C,
+          int ldc, const float* bias, int M, int N, int epi, int act = ACT_NONE) {
+  launch_gemm(gemm_args(elem, ws, A, lda, W, K, C, ldc, bias, M, N, epi, act), st, lt);
 }
 
 }  // namespace
@@ -659,7 +669,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
         gemm_launch(g, stream);
       });
     } else {
-      op("wqkv", [&] { gemm(elem, stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
+      op("wqkv", [&] { gemm(elem, set.blaslt, stream, a.ws, a.x, d, L.wqkv, d, a.qkv, 3 * d, nullptr, T, 3 * d, EPI_BF16); });
       op("split_rope", [&] { split_rope_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, vt_ld(T), stream, elem); });
     }
     op(L.local ? "attn_local" : "attn_global", [&] {
@@ -690,15 +700,15 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       op("wo", [&] { gemm_launch_partials(gwo, stream); });
       op("mlp_norm", [&] { splitk_resid_ln_launch(a.ws, gwo.splits, nullptr, a.h, L.mlp_norm, eps, T, d, a.x, stream, elem); });
     } else {
-      op("wo", [&] { gemm_launch(gwo, stream); });
+      op("wo", [&] { launch_gemm(gwo, stream, set.blaslt); });
       op("mlp_norm", [&] {
         layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
     }
     if (set.fusegeglu) {
-      op("wi_geglu", [&] { gemm(elem, stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
+      op("wi_geglu", [&] { gemm(elem, set.blaslt, stream, a.ws, a.x, d, L.wi, d, a.act, I, nullptr, T, 2 * I, EPI_GEGLU); });
     } else {
-      op("wi", [&] { gemm(elem, stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
+      op("wi", [&] { gemm(elem, set.blaslt, stream, a.ws, a.x, d, L.wi, d, a.mid, 2 * I, nullptr, T, 2 * I, EPI_BF16); });
       op("geglu", [&] { geglu_launch(a.mid, T, I, a.act, stream, elem); });
     }
     // h = h + act . Wo2^T (lib.rs:1675), and the next layer's x = attn_norm(h) (lib.rs:1592-1595)
@@ -709,7 +719,7 @@ void Model::run_encoder(const Plan& p, const Acts& a) {
       op("attn_norm", [&] { splitk_resid_ln_launch(a.ws, gwo2.splits, nullptr, a.h, next_norm, eps, T, d, a.x, stream, elem); });
       x_ready = true;
     } else {
-      op("wo2", [&] { gemm_launch(gwo2, stream); });
+      op("wo2", [&] { launch_gemm(gwo2, stream, set.blaslt); });
     }
   }
 }
@@ -839,12 +849,12 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         at.scale = hscale;
         attn_launch(at, stream);
       });
-      op("head_out_proj", [&] { gemm(elem, stream, a.ws, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(elem, set.blaslt, stream, a.ws, a.att, d, Hw.out_w, d, a.hh, d, Hw.out_b, T, d, EPI_RESID); });
       op("head_norm2", [&] {
         layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, a.x, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
-      op("head_linear1", [&] { gemm(elem, stream, a.ws, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(elem, stream, a.ws, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(elem, set.blaslt, stream, a.ws, a.x, d, Hw.l1_w, d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(elem, set.blaslt, stream, a.ws, a.mid, 4 * d, Hw.l2_w, 4 * d, a.hh, d, Hw.l2_b, T, d, EPI_RESID); });
     } else {
       // headprune (lib.rs:1728-1748): every token supplies k and v; queries, out_proj, norm2 and
       // the FFN run at rows {0, markers} only.
@@ -872,12 +882,12 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
         attn_launch(at, stream);
       });
       op("head_pick", [&] { gather_f32_launch(a.hh, picked, P, d, a.hp, stream); });
-      op("head_out_proj", [&] { gemm(elem, stream, a.ws, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
+      op("head_out_proj", [&] { gemm(elem, set.blaslt, stream, a.ws, a.attp, d, Hw.out_w, d, a.hp, d, Hw.out_b, P, d, EPI_RESID); });
       op("head_norm2", [&] {
         layernorm_launch(a.hp, nullptr, Hw.n2w, Hw.n2b, 1e-5f, P, d, a.xp, nullptr, nullptr, nullptr, nullptr, stream, elem);
       });
-      op("head_linear1", [&] { gemm(elem, stream, a.ws, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
-      op("head_linear2", [&] { gemm(elem, stream, a.ws, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
+      op("head_linear1", [&] { gemm(elem, set.blaslt, stream, a.ws, a.xp, d, Hw.l1_w, d, a.midp, 4 * d, Hw.l1_b, P, 4 * d, EPI_BF16, ACT_RELU); });
+      op("head_linear2", [&] { gemm(elem, set.blaslt, stream, a.ws, a.midp, 4 * d, Hw.l2_w, 4 * d, a.hp, d, Hw.l2_b, P, d, EPI_RESID); });
     }
   }
   // score (lib.rs:1768-1800): LN_b at the marker rows, scorer1 + GELU, scorer3; pooled row 0.
@@ -888,7 +898,7 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
     op("scorer_norm", [&] {
       layernorm_launch(src, srows, sc0_w, sc0_b, 1e-5f, R, d, a.sx, nullptr, nullptr, nullptr, nullptr, stream, elem);
     });
-    op("scorer1", [&] { gemm(elem, stream, a.ws, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
+    op("scorer1", [&] { gemm(elem, set.blaslt, stream, a.ws, a.sx, d, sc1_w, d, a.s1, S, sc1_b, R, S, EPI_BF16, ACT_GELU); });
     op("scorer3", [&] { rowdot_launch(a.s1, sc3_w, sc3_b, R, S, a.logits, stream, elem); });
   }
   op("pooled", [&] { gather_f32_launch(src, prows, n, d, a.pooled, stream); });
