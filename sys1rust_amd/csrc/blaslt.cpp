@@ -38,8 +38,16 @@ struct LtPlan {
 };
 
 std::mutex g_mu;
-std::vector<std::pair<int, hipblasLtHandle_t>> g_handles;  // one per device
-std::vector<LtPlan> g_plans;
+std::vector<std::pair<int, hipblasLtHandle_t>> g_handles;  // one per device, kept for the process
+std::vector<LtPlan> g_plans;                               // by first use; the oldest go first
+constexpr size_t kMaxPlans = 256;                          // batch sizes vary: keep the cache bounded
+
+void destroy(LtPlan& p) {
+  if (p.la) (void)hipblasLtMatrixLayoutDestroy(p.la);
+  if (p.lb) (void)hipblasLtMatrixLayoutDestroy(p.lb);
+  if (p.lc) (void)hipblasLtMatrixLayoutDestroy(p.lc);
+  if (p.op) (void)hipblasLtMatmulDescDestroy(p.op);
+}
 
 void lt_check(hipblasStatus_t s, const char* what) {
   if (s != HIPBLAS_STATUS_SUCCESS) fail(kBackend, std::string("hipBLASLt ") + what + " failed (status " + std::to_string(int(s)) + ")");
@@ -90,6 +98,10 @@ LtPlan& plan_for(const LtKey& k, hipblasLtHandle_t h) {
         p.algo = res[i].algo;
         p.ok = true;
       }
+  if (g_plans.size() >= kMaxPlans) {
+    destroy(g_plans.front());
+    g_plans.erase(g_plans.begin());
+  }
   g_plans.push_back(p);
   return g_plans.back();
 }
