@@ -165,14 +165,17 @@ def main() -> int:
                             "tokens_per_s": round(tb.total_tokens() / (tms * 1e-3))}
         print(f"[bench] {name}: {tms:.2f} ms for {tb.n} rows, {tb.total_tokens()} tokens", file=sys.stderr, flush=True)
 
-    # The f16 element type (setting dtype=f16, the real checkpoints' own type) on the headline
-    # workload, for context: same kernels, f16 MFMA and conversions.
-    if not args.no_context and "dtype" not in args.settings:
-        fmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in ["dtype=f16", args.settings] if x))
-        fms, _ = run(b, args.steps, args.warmup, model=fmodel)
-        fmodel.close()
-        throughput[args.workload + "_f16"] = {"ms_per_request": round(fms, 4), "settings": "dtype=f16"}
-        print(f"[bench] {args.workload} with dtype=f16: {fms:.3f} ms/request", file=sys.stderr, flush=True)
+    # Two opt-in settings on the headline workload, for context: the f16 element type
+    # (dtype=f16, the real checkpoints' own type; same kernels, f16 MFMA and conversions) and
+    # hipBLASLt for the unsplit residual GEMMs (blaslt).
+    for extra in ([] if args.no_context else ["dtype=f16", "blaslt"]):
+        if extra.split("=")[0] in args.settings:
+            continue
+        xmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in [extra, args.settings] if x))
+        xms, _ = run(b, args.steps, args.warmup, model=xmodel)
+        xmodel.close()
+        throughput[f"{args.workload}_{extra.replace('=', '_')}"] = {"ms_per_request": round(xms, 4), "settings": extra}
+        print(f"[bench] {args.workload} with {extra}: {xms:.3f} ms/request", file=sys.stderr, flush=True)
 
     # Kernel timing: the same steps on a second instance with the `ops` setting, which records a
     # HIP event pair around every launch on the model's stream (and so runs without graphs).

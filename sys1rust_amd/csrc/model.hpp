@@ -25,7 +25,7 @@ struct Settings {
   bool fuseln = true;      // a split-K Wo / Wo2 finishes in the kernel of the LayerNorm after it
   bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
   bool f16 = false;        // dtype=f16: weights and activations in f16 (the checkpoint's type), not bf16
-  bool blaslt = true;      // unsplit residual GEMMs of >= LT_MIN_M rows through hipBLASLt
+  bool blaslt = false;     // opt-in: unsplit residual GEMMs of >= LT_MIN_M rows through hipBLASLt
   size_t pad = 1;          // padded_len multiple
   std::vector<size_t> buckets;
   static Settings parse(const std::string& spec);

@@ -290,27 +290,28 @@ def test_fused_split_k_layernorm_bit_exact(large):
 
 
 def test_blaslt_residual_gemms_agree_and_replay(large):
-    """From 2048 rows the unsplit residual GEMMs run in hipBLASLt (setting blaslt): the answers
-    agree with the hand-written kernels' (blaslt=0) at the gates, and graph replays of that path
-    (first sight eager, then captured, then replayed) give the eager run's bits."""
+    """With the opt-in setting blaslt, from 2048 rows the unsplit residual GEMMs run in hipBLASLt:
+    the answers agree with the hand-written kernels' (the default) at the gates, and graph
+    replays of that path (first sight eager, then captured, then replayed) give the eager run's
+    bits."""
     m, o = large
-    assert "blaslt" in m.active_kernels()
+    assert "blaslt" not in m.active_kernels()
     st = synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
-    own = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="blaslt=0")
-    eager = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="graphs=0")
-    assert "blaslt" not in own.active_kernels()
+    lt = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="blaslt")
+    eager = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings="blaslt,graphs=0")
+    assert "blaslt" in lt.active_kernels()
     b = workload("state512_10q", seed=4)
     say(f"blaslt: T={b.total_tokens()}")
     want = eager.forward(b)
     for i in range(4):
-        out = m.forward(b)
+        out = lt.forward(b)
         assert np.array_equal(out.logits, want.logits) and np.array_equal(out.pooled, want.pooled), i
-    alt = own.forward(b)
-    check_answers(want.logits, alt.logits, b, "blaslt vs own kernels")
-    assert np.linalg.norm(want.pooled - alt.pooled) / np.linalg.norm(alt.pooled) <= 1e-2
-    h1, h2 = m.encoder_hidden(b), own.encoder_hidden(b)
+    own = m.forward(b)
+    check_answers(want.logits, own.logits, b, "blaslt vs own kernels")
+    assert np.linalg.norm(want.pooled - own.pooled) / np.linalg.norm(own.pooled) <= 1e-2
+    h1, h2 = lt.encoder_hidden(b), m.encoder_hidden(b)
     assert np.linalg.norm(h1 - h2) / np.linalg.norm(h2) <= 1e-2
-    own.close()
+    lt.close()
     eager.close()
 
 
