@@ -442,7 +442,8 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
 // workgroups on each of its 256 CUs):
 //   small  (one request of up to ~1000 tokens, or fewer than 200 128 x 128 tiles): 64 x 128
 //          tiles in 4 waves of 32 x 64 with three k-tiles in flight (72 KiB of LDS, two
-//          workgroups per CU); these GEMMs stream their weights, so load depth matters more than
+//          workgroups per CU), or four (96 KiB, one per CU) when the launch has at most 256
+//          workgroups; these GEMMs stream their weights, so load depth matters more than
 //          operand reuse;
 //   wide   (at least 400 192 x 128 tiles, e.g. Wqkv and Wi at a 10-question request): 192 x 128
 //          tiles in 4 waves of 96 x 64, two stages (80 KiB, two per CU, the whole LDS). Per
@@ -472,7 +473,14 @@ inline int tile_m_of(int M, int N) {
 template <class E, int EPI>
 void launch_te(const GemmArgs& g, hipStream_t st) {
   switch (tile_cfg(g.M, g.N)) {
-    case TC_SMALL: launch_t<E, 64, 128, 64, 3, 2, 2, EPI>(g, st); break;
+    case TC_SMALL:
+      // Four k-tiles in flight when the launch fits one workgroup per CU (96 KiB of LDS each):
+      // deeper prefetch for the weight stream; otherwise three, two workgroups per CU.
+      if ((long long)((g.M + 63) / 64) * (g.N / 128) * g.splits <= 256)
+        launch_t<E, 64, 128, 64, 4, 2, 2, EPI>(g, st);
+      else
+        launch_t<E, 64, 128, 64, 3, 2, 2, EPI>(g, st);
+      break;
     case TC_WIDE: launch_t<E, 192, 128, 64, 2, 2, 2, EPI>(g, st); break;
     case TC_MID: launch_t<E, 64, 128, 64, 2, 2, 2, EPI>(g, st); break;
   }
