@@ -577,8 +577,8 @@ GemmPlan gemm_plan(int M, int N, int K, bool reduce_folded) {
   const int bm = tile_m_of(M, N);
   const int tiles = ((M + bm - 1) / bm) * (N / 128);
   const int KT = K / BK;
-  // Few tiles (a short request on a narrow output): split K so that about 256 workgroups run,
-  // each keeping at least 4 k-tiles, and the f32 partials (s M N 4 bytes, written and read
+  // Few tiles (a short request on a narrow output): split K so that up to 256 workgroups run
+  // (one per CU, which takes the four-deep pipeline), each keeping at least 4 k-tiles, and the f32 partials (s M N 4 bytes, written and read
   // back) stay within twice the weight bytes (N K 2) the GEMM streams anyway, or eight times
   // them when the reduce is folded. The partials need a second pass: a reduce kernel of its own
   // (about as long as a whole-K pass over 32-95 tiles saves, launch included), unless the
@@ -586,7 +586,7 @@ GemmPlan gemm_plan(int M, int N, int K, bool reduce_folded) {
   // little. So split below 96 tiles when folded, below 32 otherwise.
   int s = 1;
   if (tiles < (reduce_folded ? 96 : 32))
-    s = std::max(1, std::min({KT / 4, (256 + tiles - 1) / tiles, (reduce_folded ? 4 : 1) * K / std::max(M, 1)}));
+    s = std::max(1, std::min({KT / 4, std::max(1, 256 / tiles), (reduce_folded ? 4 : 1) * K / std::max(M, 1)}));
   p.splits = s;
   p.ws_floats = s > 1 ? size_t(s) * M * N : 0;
   return p;
