@@ -27,7 +27,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "ms/request (128 & 512 tok, 1 & 10 questions); GEMM MFMA util %"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
-BASELINE_M5_10Q512_MS = 379.0  # sys1rust on an Apple M5, README.md:111
+REFERENCE_M5_10Q512_MS = 379.0  # sys1rust on an Apple M5, README.md:111
 
 
 def gemm_flops(name: str, T: int, P: int, R: int, d: int, I: int, S: int) -> float:
@@ -102,7 +102,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by request with no collective, see DESIGN.md)", file=sys.stderr)
+              "(the path shards by request with no collective)", file=sys.stderr)
         return 2
 
     import torch
@@ -300,7 +300,7 @@ def main() -> int:
         "ms_per_step": round(ms, 4),
         "higher_is_better": False,
         "scaling": "weak",
-        "vs_baseline": round(ms / BASELINE_M5_10Q512_MS, 5),
+        "vs_baseline": round(ms / REFERENCE_M5_10Q512_MS, 5),
         "dtype": "f16" if model.name().endswith(",f16)") else "bf16",
         "data": "synthetic",
         "config": {"workload": f"{args.workload}: encoder+head+scorer forward and answer decode, ModernBERT-large "

@@ -1,6 +1,6 @@
 """End-to-end parity of the HIP forward against the oracle, through the C ABI (HipBackend).
 
-Gates (the north star's): identical argmax choice per choice question, answer probabilities
+Gates: identical argmax choice per choice question, answer probabilities
 within 5e-3 absolute (after the f64 temperature softmax of decode.rs), and final hidden states
 within 2e-2 relative (per real token, ||gpu - oracle|| / ||oracle||). The oracle is float32 with
 the same bf16 weights; the GPU computes in bf16 with f32 accumulation and an f32 residual stream.
