@@ -188,13 +188,14 @@ def test_f16_model_keeps_f16_checkpoint_bits(small_model):
     c.close()
 
 
-def test_graph_replays_match_eager_runs(small_model):
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_graph_replays_match_eager_runs(small_model, dtype):
     """Repeated shapes replay a captured HIP graph: every replay, interleaved with other shapes
     and with eager work, gives the eager path's bits."""
     cfg, agent, st, b, z = small_model
-    say("graphs: replay vs eager")
-    g = HipBackend(st, json.dumps(cfg), json.dumps(agent))
-    e = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="graphs=0")
+    say(f"graphs: replay vs eager ({dtype})")
+    g = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=f"dtype={dtype}")
+    e = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=f"dtype={dtype},graphs=0")
     b2 = b.rows([1, 2])
     want = {0: e.forward(b), 1: e.forward(b2)}
     want_h = e.encoder_hidden(b)
