@@ -132,8 +132,8 @@ int s1k_qkv_rope(const void* A, const void* W, int M, int d, const int32_t* pos,
                  void* q, void* k, void* v, int v_ld, void* stream);
 
 /* Standalone split + RoPE pass: qkv [M, 3d] bf16 -> q, k [d/64, M, 64] bf16 and v transposed
- * [d/64, 64, v_ld] bf16 (v_ld at least M rounded up to 8; v columns from M up to that are
- * written as zeros). theta <= 0 means no rotation (the decision head's split). */
+ * [d/64, 64, v_ld] bf16 (v_ld a multiple of 8, at least M rounded up to 8; v columns from M
+ * up to that are written as zeros). theta <= 0 means no rotation (the decision head's split). */
 int s1k_split_rope(const void* qkv, int M, int d, const int32_t* pos, double theta, void* q,
                    void* k, void* v, int v_ld, void* stream);
 

@@ -353,7 +353,8 @@ int s1k_split_rope(const void* qkv, int M, int d, const int32_t* pos, double the
   return guard([&] {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (d % 64) s1::fail(s1::kConfig, "s1k_split_rope: d must be a multiple of 64");
-    if (v_ld < (M + 7) / 8 * 8) s1::fail(s1::kConfig, "s1k_split_rope: v_ld must be at least M rounded up to 8");
+    if (v_ld < (M + 7) / 8 * 8 || v_ld % 8)
+      s1::fail(s1::kConfig, "s1k_split_rope: v_ld must be a multiple of 8 and at least M rounded up to 8");
     const float* c = nullptr;
     const float* s = nullptr;
     if (theta > 0) {

@@ -185,75 +185,84 @@ __global__ __launch_bounds__(256) void splitk_resid_ln_kernel(const float* __res
     *reinterpret_cast<uint4*>(y + size_t(row) * d + c * 512 + lane * 8) = pack8<E>(o + c * 8);
 }
 
-// One thread per (token, head, quarter of the 32 rotation pairs): pairs i0 .. i0 + 7 with
-// i0 = 8 * quarter, i.e. dims [i0, i0 + 8) and [i0 + 32, i0 + 40) of the head, for q, k and v.
+// The standalone split + RoPE pass, one workgroup per (64-token block, head), 256 threads:
+// thread (token t0 + tid / 4, quarter) takes rotation pairs i0 .. i0 + 7 (i0 = 8 quarter), i.e.
+// dims [i0, i0 + 8) and [i0 + 32, i0 + 40) of the head, for q and k. The 4 threads of a token
+// read the head's 128 bytes of its qkv row and write them to the head-major q / k, where the
+// block's 64 tokens are one contiguous 8 KiB run. v goes through LDS, [token][dim], and leaves
+// transposed as 16-byte pieces of 8 tokens: 128-byte rows of [H, 64, ldv].
 template <class E>
 __global__ __launch_bounds__(256) void split_rope_kernel(const uint16_t* __restrict__ qkv, int T, int d,
                                                         const int* __restrict__ pos, const float* __restrict__ ct,
                                                         const float* __restrict__ stab, uint16_t* __restrict__ q,
                                                         uint16_t* __restrict__ k, uint16_t* __restrict__ v,
                                                         int ldv) {
+  constexpr int VP = 64 + 8;  // LDS row pitch of the v block, elements (16 bytes of padding)
+  __shared__ __attribute__((aligned(16))) uint16_t sv[64 * VP];
   const int H = d >> 6;
-  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (long long)T * H * 4) return;
-  const int quarter = int(gid & 3);
-  const int head = int((gid >> 2) % H);
-  const int t = int((gid >> 2) / H);
+  const int head = blockIdx.x % H;
+  const int t0 = (blockIdx.x / H) * 64;
+  const int tl = threadIdx.x >> 2, quarter = threadIdx.x & 3;
+  const int t = t0 + tl;
   const int i0 = quarter * 8;
-  const uint16_t* src = qkv + size_t(t) * 3 * d + head * 64 + i0;
-  const size_t dst = (size_t(head) * T + t) * 64 + i0;
-  float c[8], s[8];
-  const bool rope = ct != nullptr;
-  if (rope) {
-    const int p = pos[t];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      c[j] = ct[p * 32 + i0 + j];
-      s[j] = stab[p * 32 + i0 + j];
+  if (t < T) {
+    const uint16_t* src = qkv + size_t(t) * 3 * d + head * 64 + i0;
+    const size_t dst = (size_t(head) * T + t) * 64 + i0;
+    float c[8], s[8];
+    const bool rope = ct != nullptr;
+    if (rope) {
+      const int p = pos[t];
+      const float4* cp = reinterpret_cast<const float4*>(ct + p * 32 + i0);
+      const float4* sp = reinterpret_cast<const float4*>(stab + p * 32 + i0);
+      const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+      c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+      s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w; s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
     }
-  }
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const uint16_t* sp = src + part * d;
-    uint16_t* dp = (part == 0 ? q : k) + dst;
-    const uint4 a = *reinterpret_cast<const uint4*>(sp);
-    const uint4 b = *reinterpret_cast<const uint4*>(sp + 32);
-    if (!rope) {
-      *reinterpret_cast<uint4*>(dp) = a;
-      *reinterpret_cast<uint4*>(dp + 32) = b;
-      continue;
-    }
-    float x1[8], x2[8], y1[8], y2[8];
-    unpack8<E>(a, x1);
-    unpack8<E>(b, x2);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      y1[j] = x1[j] * c[j] - x2[j] * s[j];
-      y2[j] = x1[j] * s[j] + x2[j] * c[j];
-    }
-    *reinterpret_cast<uint4*>(dp) = pack8<E>(y1);
-    *reinterpret_cast<uint4*>(dp + 32) = pack8<E>(y2);
-  }
-  // v, transposed: dims i0 .. i0 + 7 and i0 + 32 .. i0 + 39 of token t.
-  const uint16_t* sv = src + 2 * d;
-  const uint4 va = *reinterpret_cast<const uint4*>(sv);
-  const uint4 vb = *reinterpret_cast<const uint4*>(sv + 32);
-  uint16_t* vt = v + (size_t(head) * 64 + i0) * ldv + t;
-  const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    vt[size_t(2 * j) * ldv] = uint16_t(wa[j]);
-    vt[size_t(2 * j + 1) * ldv] = uint16_t(wa[j] >> 16);
-    vt[size_t(32 + 2 * j) * ldv] = uint16_t(wb[j]);
-    vt[size_t(33 + 2 * j) * ldv] = uint16_t(wb[j] >> 16);
-  }
-  if (t == T - 1)  // zeros up to the next multiple of 8 tokens, as the fused path writes them
-    for (int c = 1; t + c < (T + 7) / 8 * 8; ++c)
+    for (int part = 0; part < 2; ++part) {
+      const uint16_t* sp = src + part * d;
+      uint16_t* dp = (part == 0 ? q : k) + dst;
+      const uint4 a = *reinterpret_cast<const uint4*>(sp);
+      const uint4 b = *reinterpret_cast<const uint4*>(sp + 32);
+      if (!rope) {
+        *reinterpret_cast<uint4*>(dp) = a;
+        *reinterpret_cast<uint4*>(dp + 32) = b;
+        continue;
+      }
+      float x1[8], x2[8], y1[8], y2[8];
+      unpack8<E>(a, x1);
+      unpack8<E>(b, x2);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        vt[size_t(j) * ldv + c] = 0;
-        vt[size_t(32 + j) * ldv + c] = 0;
+        y1[j] = x1[j] * c[j] - x2[j] * s[j];
+        y2[j] = x1[j] * s[j] + x2[j] * c[j];
       }
+      *reinterpret_cast<uint4*>(dp) = pack8<E>(y1);
+      *reinterpret_cast<uint4*>(dp + 32) = pack8<E>(y2);
+    }
+    const uint16_t* sv_src = src + 2 * d;
+    *reinterpret_cast<uint4*>(&sv[tl * VP + i0]) = *reinterpret_cast<const uint4*>(sv_src);
+    *reinterpret_cast<uint4*>(&sv[tl * VP + i0 + 32]) = *reinterpret_cast<const uint4*>(sv_src + 32);
+  } else {
+    // Tokens past T read as zeros: the piece holding token T - 1 writes them into the columns up
+    // to the next multiple of 8, which every v writer leaves zero.
+    *reinterpret_cast<uint4*>(&sv[tl * VP + i0]) = make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&sv[tl * VP + i0 + 32]) = make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  const int tend = (T + 7) / 8 * 8;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int p = threadIdx.x + it * 256;
+    const int dim = p >> 3, c8 = p & 7;  // tokens t0 + 8 c8 .. + 7 of dim `dim`
+    const int tt = t0 + 8 * c8;
+    if (tt >= tend) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = uint32_t(sv[(8 * c8 + 2 * j) * VP + dim]) | (uint32_t(sv[(8 * c8 + 2 * j + 1) * VP + dim]) << 16);
+    *reinterpret_cast<uint4*>(v + (size_t(head) * 64 + dim) * ldv + tt) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
 }
 
 template <class E>
@@ -377,9 +386,8 @@ void splitk_resid_ln_launch(const float* ws, int splits, const float* bias, floa
 
 void split_rope_launch(const uint16_t* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t,
                        uint16_t* q, uint16_t* k, uint16_t* v, int ldv, hipStream_t st, int elem) {
-  const long long n = (long long)T * (d / 64) * 4;
-  if (n <= 0) return;
-  const dim3 grid(unsigned((n + 255) / 256)), block(256);
+  if (T <= 0) return;
+  const dim3 grid(unsigned((T + 63) / 64 * (d / 64))), block(256);
   if (elem == ELEM_F16)
     hipLaunchKernelGGL(split_rope_kernel<F16>, grid, block, 0, st, qkv, T, d, pos, cos_t, sin_t, q, k, v, ldv);
   else

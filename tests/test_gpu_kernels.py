@@ -171,10 +171,11 @@ def test_fused_wqkv_split_rope(dev, theta, M):
         assert np.all(err <= np.abs(ref) * 2 ** -8 + 2e-4), float(err.max())
 
 
+@pytest.mark.parametrize("M", [700, 5, 64])
 @pytest.mark.parametrize("theta", [160000.0, 10000.0, 0.0])
-def test_split_rope_pass(dev, theta):
-    say(f"split_rope theta={theta}")
-    M, d = 700, 1024
+def test_split_rope_pass(dev, theta, M):
+    say(f"split_rope theta={theta} M={M}")
+    d = 1024
     g = torch.Generator(device="cpu").manual_seed(3)
     qkv = bf16_bits(torch.randn(M, 3 * d, generator=g)).to(dev)
     pos = torch.arange(M, dtype=torch.int32, device=dev) * 11  # positions up to 7689
