@@ -38,6 +38,18 @@ def test_library_exports_every_declared_symbol():
     assert set(_lib.SIGNATURES) == set(names)
 
 
+@pytest.mark.parametrize("M,d,v_ld,needle", [
+    (10, 1000, 24, "d must be a multiple of 64"),
+    (10, 1024, 8, "v_ld must be a multiple of 8"),   # below M rounded up to 8
+    (10, 1024, 20, "v_ld must be a multiple of 8"),  # 16-byte V^T stores need 8-element rows
+])
+def test_split_rope_entry_checks_shapes_before_any_launch(M, d, v_ld, needle):
+    # The checks come before any device call, so null pointers never reach a kernel.
+    with pytest.raises(S1Error) as e:
+        check(_lib.lib().s1k_split_rope(None, M, d, None, 0.0, None, None, None, v_ld, None))
+    assert e.value.kind == "Config" and needle in str(e.value)
+
+
 SMALL = json.dumps(small_config(layers=2, vocab=512))
 
 
