@@ -8,10 +8,15 @@ The headline workload is a 512-token state with 10 questions on the ModernBERT-l
 The model runs sys1rust's production settings string (DEFAULT_TUNING, the BackendOptions::tuning
 of every served model, runtime/crates/sys1rust/src/config.rs:29) unless --settings says otherwise.
 
+The decode is decode.rs's (decode_answers with the action head, decode.rs:309-399), restated in
+numpy. Each shape of the metric (1 question over 128 and over 512 tokens, 10 questions over 512)
+is reported with the mean, median, min and max per request, the GPU forward alone (the s1_forward
+call: batch tables up, the forward, outputs back) and the decode alone.
+
 Printed: one JSON line with the metric, `roofline` for the dominant kernel (algorithmic FLOPs per
 launch / the kernel's mean duration, from HIP events recorded on the model's stream around each
-launch during the timed steps), and `cpu_baseline` (the oracle, numpy f32, on a bounded sample
-of the same workload on this host's cores: the median of repeated timings after warm-ups).
+launch during the timed steps), and `cpu_baseline` (the oracle's forward in torch float32 on this
+host's cores, whole requests of each shape: the median of repeated timings after warm-ups).
 """
 from __future__ import annotations
 
@@ -106,67 +111,90 @@ def host_cpu() -> dict:
     return {"host_cpus": usable, "cpu_model": model}
 
 
-def cpu_baseline(ckpt: bytes, b, args) -> dict:
-    """The reference's forward restated on the CPU (the oracle: numpy f32 over OpenBLAS), timed on
-    a bounded sample of the workload: `--cpu-rows` of its rows (rows are independent, so the
-    request's time is the sample's times n / rows), 3 warm-ups then the median of
-    `--cpu-repeats` runs on every BLAS thread; then 1 warm-up and the median of 5 runs on 4
-    threads, the thread count of the published upstream fp32 CPU figures."""
+CPU_SHAPES = ["state128_1q", "state512_1q", "state512_10q"]
+
+
+def cpu_baseline(ckpt: bytes, args) -> dict:
+    """The reference's CPU path restated: the oracle's forward in torch float32 on the host
+    (TorchOracle.forward_batched: the padded batch per layer with the dense masks and the pruned
+    last head layer, as MlxBackend::forward runs on BackendOptions device Cpu), then the answer
+    decode with the action head, for whole requests of each shape of the metric. On every usable
+    host thread: 3 warm-ups, then the median of `--cpu-repeats` runs per shape; then on 4 threads
+    (the thread count of the published upstream fp32 CPU figures): 1 warm-up and the median of a
+    few runs per shape (3 for the 10-question request, which takes seconds)."""
     import statistics
 
+    import torch
+
     from oracle.oracle import Oracle
-    from sys1rust_amd.decode import decode_answers
-    from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE
+    from oracle.torch_ref import TorchOracle
+    from sys1rust_amd.decode import ActHead, decode_answers
+    from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, workload
 
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
+    hc = host_cpu()
+    threads = hc["host_cpus"]
+    t = TorchOracle(Oracle(ckpt, MODERNBERT_LARGE, AGENT), "cpu")
+    act = ActHead.from_safetensors(ckpt)
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threadpool_limits = None
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    o = Oracle(ckpt, MODERNBERT_LARGE, AGENT)
-    rows = list(range(min(args.cpu_rows, b.n)))
-    sub = b.rows(rows)
+    def once(b) -> float:
+        t0 = time.perf_counter()
+        with torch.inference_mode():
+            lg, pl = t.forward_batched(b)
+        decode_answers(lg, b.kmax, b.marker_count, b.qtype, pooled=pl, act_head=act)
+        return (time.perf_counter() - t0) * 1e3
 
-    def once() -> float:
-        t = time.perf_counter()
-        lg, _ = o.forward(sub)
-        decode_answers(lg, sub.kmax, sub.marker_count, sub.qtype)
-        return (time.perf_counter() - t) * 1e3 * b.n / len(rows)
-
-    def timed(warm: int, reps: int) -> list:
+    def timed(b, warm: int, reps: int) -> list:
         for _ in range(warm):
-            once()
-        return [once() for _ in range(reps)]
+            once(b)
+        return [once(b) for _ in range(reps)]
 
-    runs = timed(3, args.cpu_repeats)
-    med = statistics.median(runs)
-    cpu = {
-        "value": round(med, 1),
+    shapes = {}
+    prev = torch.get_num_threads()
+    try:
+        for nth in (threads, 4):
+            torch.set_num_threads(nth)
+            for name in CPU_SHAPES:
+                b = workload(name, seed=args.seed)
+                if nth == threads:
+                    runs = timed(b, 3, args.cpu_repeats)
+                else:
+                    runs = timed(b, 1, 3 if b.n > 1 else 10)
+                key = "all_threads" if nth == threads else "4_threads"
+                shapes.setdefault(name, {})[key] = {"median_ms": round(statistics.median(runs), 1),
+                                                    "min_ms": round(min(runs), 1), "max_ms": round(max(runs), 1),
+                                                    "repeats": len(runs), "threads": nth}
+                print(f"[bench] cpu baseline {name}: {statistics.median(runs):.1f} ms/request on {nth} threads "
+                      f"(median of {len(runs)}, {min(runs):.1f}-{max(runs):.1f})", file=sys.stderr, flush=True)
+            if threads <= 4:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    head = shapes[args.workload]["all_threads"] if args.workload in shapes else None
+    return {
+        "value": head["median_ms"] if head else None,
         "unit": "ms/request",
         "cores": threads,
         "kind": "port",
-        "label": f"reference CPU path, restated (numpy f32, {threads} cores)",
-        "sample": f"{len(rows)} of the {b.n} rows of one {args.workload} request through the oracle (encoder, "
-                  f"head, scorer, decode) with dense local-attention masks as the reference's CPU path runs "
-                  f"them at this length (dense_upto=1024), scaled by {b.n} / {len(rows)}; median of "
-                  f"{len(runs)} runs after 3 warm-ups",
-        "repeats": len(runs),
-        "min": round(min(runs), 1),
-        "max": round(max(runs), 1),
-        **host_cpu(),
+        "label": f"reference CPU path, restated (torch f32, {threads} threads)",
+        "sample": f"whole requests of {', '.join(CPU_SHAPES)} (the same seeded inputs as the GPU lines): the "
+                  f"padded batch through the encoder, the pruned decision head and the scorer with dense "
+                  f"local-attention masks (dense_upto=1024), then the answer decode with the action head; "
+                  f"median of {args.cpu_repeats} runs after 3 warm-ups on {threads} threads, and of 10 (3 for "
+                  f"10 questions) after 1 on 4 threads",
+        "repeats": head["repeats"] if head else None,
+        "min": head["min_ms"] if head else None,
+        "max": head["max_ms"] if head else None,
+        "shapes": shapes,
+        **hc,
     }
-    print(f"[bench] cpu baseline {cpu['value']} ms/request on {threads} threads "
-          f"(median of {len(runs)}, {cpu['min']}-{cpu['max']})", file=sys.stderr, flush=True)
-    if threadpool_limits is not None and threads > 4:
-        with threadpool_limits(limits=4, user_api="blas"):
-            r4 = timed(1, 5)
-        cpu["value_4_threads"] = round(statistics.median(r4), 1)
-        cpu["repeats_4_threads"] = len(r4)
-        print(f"[bench] cpu baseline {cpu['value_4_threads']} ms/request on 4 threads (median of 5)",
-              file=sys.stderr, flush=True)
-    return cpu
+
+
+def summary(runs: list) -> dict:
+    """Mean, median, min and max (ms) of per-step times."""
+    import statistics
+
+    return {"mean": round(sum(runs) / len(runs), 4), "median": round(statistics.median(runs), 4),
+            "min": round(min(runs), 4), "max": round(max(runs), 4)}
 
 
 def main() -> int:
@@ -177,8 +205,8 @@ def main() -> int:
     ap.add_argument("--workload", default="state512_10q")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload the CPU baseline runs")
-    ap.add_argument("--cpu-repeats", type=int, default=20, help="timed CPU baseline runs (after 3 warm-ups)")
+    ap.add_argument("--cpu-repeats", type=int, default=20,
+                    help="timed CPU baseline runs per shape on every host thread (after 3 warm-ups)")
     ap.add_argument("--settings", default=None, help="settings string (default: sys1rust's DEFAULT_TUNING)")
     ap.add_argument("--no-context", action="store_true",
                     help="time only the headline workload (no 1-question shapes), e.g. under a profiler")
@@ -194,7 +222,7 @@ def main() -> int:
     import torch
 
     from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
-    from sys1rust_amd.decode import decode_answers
+    from sys1rust_amd.decode import ActHead, decode_answers
     from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, SCORER_WIDTH, workload
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -216,40 +244,60 @@ def main() -> int:
     print(f"[bench] model ready in {time.time() - t0:.1f}s: {model.name()} {model.active_kernels()}",
           file=sys.stderr, flush=True)
 
+    act = ActHead.from_safetensors(ckpt)
+
     def run(b, steps, warmup, model=model):
+        """`steps` requests after `warmup`: the forward (batch upload, GPU work, outputs back) and
+        the CPU answer decode with the action head. Returns the mean ms per request over the timed
+        region, the op statistics, and the per-request forward and decode times (ms)."""
         for _ in range(warmup):
             out = model.forward(b)
-            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype)
+            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype, pooled=out.pooled, act_head=act)
         model.op_stats_reset()
+        fwd, dec = [], []
         torch.cuda.synchronize()
         t = time.perf_counter()
         for _ in range(steps):
+            t0 = time.perf_counter()
             out = model.forward(b)
-            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype)
+            t1 = time.perf_counter()
+            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype, pooled=out.pooled, act_head=act)
+            t2 = time.perf_counter()
+            fwd.append((t1 - t0) * 1e3)
+            dec.append((t2 - t1) * 1e3)
         torch.cuda.synchronize()
-        return (time.perf_counter() - t) * 1e3 / steps, model.op_stats()
+        return (time.perf_counter() - t) * 1e3 / steps, model.op_stats(), fwd, dec
+
+    def shape_line(ms, fwd, dec) -> dict:
+        tot = [a + c for a, c in zip(fwd, dec)]
+        return {"ms_per_request": round(ms, 4), "request_ms": summary(tot), "gpu_forward_ms": summary(fwd),
+                "cpu_decode_ms": summary(dec)}
 
     # Context shapes (1 question at 128 and 512 tokens), then the headline workload last so its
     # per-kernel statistics are the ones reported.
-    shapes = {}
+    shapes, detail = {}, {}
     for name in ([] if args.no_context else ["state128_1q", "state512_1q"]):
         b = workload(name, seed=args.seed)
-        ms, _ = run(b, max(5, args.steps // 2), args.warmup)
+        ms, _, fwd, dec = run(b, args.steps, args.warmup)
         shapes[name] = round(ms, 4)
-        print(f"[bench] {name}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
+        detail[name] = shape_line(ms, fwd, dec)
+        print(f"[bench] {name}: {ms:.3f} ms/request (T={b.total_tokens()}); {detail[name]}", file=sys.stderr,
+              flush=True)
     b = workload(args.workload, seed=args.seed)
-    ms, _ = run(b, args.steps, args.warmup)
+    ms, _, fwd, dec = run(b, args.steps, args.warmup)
     shapes[args.workload] = round(ms, 4)
-    print(f"[bench] {args.workload}: {ms:.3f} ms/request (T={b.total_tokens()})", file=sys.stderr, flush=True)
+    detail[args.workload] = shape_line(ms, fwd, dec)
+    print(f"[bench] {args.workload}: {ms:.3f} ms/request (T={b.total_tokens()}); {detail[args.workload]}",
+          file=sys.stderr, flush=True)
 
     # Throughput context (not the metric): the 64-request varlen sweep packed into one forward,
     # and one 8192-token state.
     throughput = {}
     for name in ([] if args.no_context else ["sweep64", "state8192_1q"]):
         tb = workload(name, seed=args.seed)
-        tms, _ = run(tb, 3, 1)
-        throughput[name] = {"ms_per_batch": round(tms, 3), "rows": tb.n, "tokens": tb.total_tokens(),
-                            "sequences_per_s": round(tb.n / (tms * 1e-3), 1),
+        tms, _, tf, _ = run(tb, 3, 1)
+        throughput[name] = {"ms_per_batch": round(tms, 3), "gpu_forward_ms": summary(tf), "rows": tb.n,
+                            "tokens": tb.total_tokens(), "sequences_per_s": round(tb.n / (tms * 1e-3), 1),
                             "tokens_per_s": round(tb.total_tokens() / (tms * 1e-3))}
         print(f"[bench] {name}: {tms:.2f} ms for {tb.n} rows, {tb.total_tokens()} tokens", file=sys.stderr, flush=True)
 
@@ -260,21 +308,21 @@ def main() -> int:
         if extra.split("=")[0] in args.settings:
             continue
         xmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in [args.settings, extra] if x))
-        xms, _ = run(b, args.steps, args.warmup, model=xmodel)
-        xshapes = {}
-        for name in ["state128_1q", "state512_1q"]:
-            sms, _ = run(workload(name, seed=args.seed), max(5, args.steps // 2), args.warmup, model=xmodel)
-            xshapes[name] = round(sms, 4)
+        xdetail = {}
+        for name in ["state128_1q", "state512_1q", args.workload]:
+            xms, _, xf, xd = run(workload(name, seed=args.seed), args.steps, args.warmup, model=xmodel)
+            xdetail[name] = shape_line(xms, xf, xd)
         throughput[f"{args.workload}_{extra.replace('=', '_')}"] = {
-            "ms_per_request": round(xms, 4), "settings": extra, "shapes_ms_per_request": xshapes,
+            "ms_per_request": xdetail[args.workload]["ms_per_request"], "settings": extra,
+            "shapes_ms_per_request": {k: v["ms_per_request"] for k, v in xdetail.items()}, "shapes": xdetail,
             "active_kernels": xmodel.active_kernels()}
         xmodel.close()
-        print(f"[bench] {args.workload} with {extra}: {xms:.3f} ms/request; {xshapes}", file=sys.stderr, flush=True)
+        print(f"[bench] {args.workload} with {extra}: {xdetail}", file=sys.stderr, flush=True)
 
     # Kernel timing: the same steps on a second instance with the `ops` setting, which records a
     # HIP event pair around every launch on the model's stream (and so runs without graphs).
     kmodel = HipBackend(ckpt, enc_json, agent_json, settings=",".join(x for x in [args.settings, "ops"] if x))
-    ms_eager, stats = run(b, args.steps, args.warmup, model=kmodel)
+    ms_eager, stats, _, _ = run(b, args.steps, args.warmup, model=kmodel)
     kmodel.close()
     print(f"[bench] {args.workload}: {ms_eager:.3f} ms/request with per-kernel events", file=sys.stderr, flush=True)
 
@@ -347,7 +395,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(ckpt, b, args)
+        cpu = cpu_baseline(ckpt, args)
 
     line = {
         "metric": METRIC,
@@ -368,6 +416,7 @@ def main() -> int:
                    "settings": args.settings, "active_kernels": model.active_kernels()},
         "sequences_per_s": round(b.n / (ms * 1e-3), 1),
         "shapes_ms_per_request": shapes,
+        "shapes": detail,
         "throughput": throughput,
         "gemm_mfma_util": {k: v["mfma_util"] for k, v in gemms.items()},
         "roofline": roofline,

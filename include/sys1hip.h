@@ -163,7 +163,9 @@ int s1k_gemm(const void* A, int lda, const void* W, int ldw, void* C, int ldc, c
  * library (8 MiB per GPU, held until the process ends) instead of a workspace the library
  * allocates; every split plan fits it, and a shape that would not is refused with S1_ERR_CONFIG.
  * All calls on one GPU share that array: calls that overlap on one GPU (other streams, other
- * threads) race and must be serialised by the caller. */
+ * threads) race and must be serialised by the caller. The first call on each GPU looks up the
+ * array's device address and must not be made under graph capture (it is then refused with
+ * S1_ERR_CONFIG); later calls may be captured and replayed. */
 int s1k_gemm_noalloc(const void* A, int lda, const void* W, int ldw, void* C, int ldc, const float* bias,
                      int M, int N, int K, int epi, int act, void* stream);
 

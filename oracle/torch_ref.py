@@ -144,3 +144,87 @@ class TorchOracle:
             lg = np.where(np.arange(b.kmax) < int(b.marker_count[r]), lg, O.LOGIT_MASKED)
             logits[r * b.kmax: (r + 1) * b.kmax] = lg
         return logits, pooled.reshape(-1)
+
+    # ---- the whole padded batch at once, as the reference's CPU path runs it
+    @torch.no_grad()
+    def forward_batched(self, b, headprune: bool = True):
+        """(logits [n*kmax], pooled [n*d]) for the padded batch in one pass per layer: the
+        reference's forward as its CPU device runs it (MlxBackend::forward on BackendOptions
+        device Cpu, lib.rs:1525-1863, backend.rs:14-20): [n, len] rows with the -1e4 pad mask
+        and, on local layers, the dense window mask (dense_upto, lib.rs:1399-1417,1646-1649);
+        with headprune the last head layer keeps every key and value but runs its queries,
+        out_proj, norm2 and FFN at the scorer's rows only (lib.rs:1728-1748). The same
+        operations as the per-row methods above, through torch's fused CPU kernels (layer_norm,
+        gelu, scaled_dot_product_attention); pinned to them by tests/test_oracle.py."""
+        import torch.nn.functional as F
+
+        o, w = self.o, self.w
+        d, H, hd, n, L = o.d, o.heads, o.hd, b.n, b.len
+        ids = torch.from_numpy(b.input_ids.reshape(n, L).astype(np.int64)).to(self.dev)
+        am = torch.from_numpy(b.attention_mask.reshape(n, L).astype(np.int64)).to(self.dev)
+        neg = float(O.MASK_NEG)
+        pad = torch.where(am == 1, 0.0, neg).to(torch.float32)[:, None, None, :]  # [n, 1, 1, L]
+        idx = torch.arange(L, device=self.dev)
+        win = torch.where((idx[:, None] - idx[None, :]).abs() > o.window, neg, 0.0).to(torch.float32)
+        masks = {False: pad, True: pad + win}
+        scale = float(1.0 / np.sqrt(np.float32(hd)))
+
+        def heads(x, rows, nh):  # [n, rows, nh * 64] -> [n, nh, rows, 64]
+            return x.view(n, rows, nh, -1).transpose(1, 2)
+
+        def rope(x, cos, sin):
+            half = x.shape[-1] // 2
+            x1, x2 = x[..., :half], x[..., half:]
+            return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
+
+        h = F.layer_norm(w["encoder.embeddings.tok_embeddings.weight"][ids], (d,),
+                         w["encoder.embeddings.norm.weight"], None, o.eps)
+        for l in range(o.layers):
+            p = f"encoder.layers.{l}"
+            a = h if l == 0 else F.layer_norm(h, (d,), w[f"{p}.attn_norm.weight"], None, o.eps)
+            q, k, v = (a @ w[f"{p}.attn.Wqkv.weight"].T).split(d, dim=-1)
+            cos, sin = (t[:L] for t in self.tables[o.local[l]])
+            q, k, v = rope(heads(q, L, H), cos, sin), rope(heads(k, L, H), cos, sin), heads(v, L, H)
+            att = F.scaled_dot_product_attention(q, k, v, attn_mask=masks[o.local[l]], scale=scale)
+            h = h + att.transpose(1, 2).reshape(n, L, d) @ w[f"{p}.attn.Wo.weight"].T
+            m = F.layer_norm(h, (d,), w[f"{p}.mlp_norm.weight"], None, o.eps)
+            x, g = (m @ w[f"{p}.mlp.Wi.weight"].T).split(o.inter, dim=-1)
+            h = h + (F.gelu(x) * g) @ w[f"{p}.mlp.Wo.weight"].T
+        h = F.layer_norm(h, (d,), w["encoder.final_norm.weight"], None, o.eps)
+
+        # decision head (Oracle._head_row), rows of the scorer: position 0, then the markers
+        Hh = o.head_heads
+        h = h + w["type_emb.weight"][torch.from_numpy(b.qtype.astype(np.int64)).to(self.dev)][:, None, :]
+        kmax = b.kmax
+        pick = torch.zeros(n, 1 + kmax, dtype=torch.int64, device=self.dev)
+        if kmax:
+            pick[:, 1:] = torch.from_numpy(b.marker_pos.reshape(n, kmax).astype(np.int64)).to(self.dev)
+        for j in range(o.head_layers):
+            p = f"head.layers.{j}"
+            x = F.layer_norm(h, (d,), w[f"{p}.norm1.weight"], w[f"{p}.norm1.bias"], 1e-5)
+            wq, wk, wv = w[f"{p}.self_attn.in_proj_weight"].split(d, dim=0)
+            bq, bk, bv = w[f"{p}.self_attn.in_proj_bias"].split(d, dim=0)
+            k, v = heads(x @ wk.T + bk, L, Hh), heads(x @ wv.T + bv, L, Hh)
+            last = headprune and j == o.head_layers - 1
+            if last:  # queries and everything after them at the picked rows only
+                gidx = pick[:, :, None].expand(n, 1 + kmax, d)
+                x, h = x.gather(1, gidx), h.gather(1, gidx)
+            rows = x.shape[1]
+            q = heads(x @ wq.T + bq, rows, Hh)
+            att = F.scaled_dot_product_attention(q, k, v, attn_mask=pad, scale=1.0 / np.sqrt(d // Hh))
+            h = h + att.transpose(1, 2).reshape(n, rows, d) @ w[f"{p}.self_attn.out_proj.weight"].T \
+                + w[f"{p}.self_attn.out_proj.bias"]
+            x = F.layer_norm(h, (d,), w[f"{p}.norm2.weight"], w[f"{p}.norm2.bias"], 1e-5)
+            x = torch.clamp_min(x @ w[f"{p}.linear1.weight"].T + w[f"{p}.linear1.bias"], 0.0)
+            h = h + x @ w[f"{p}.linear2.weight"].T + w[f"{p}.linear2.bias"]
+        if h.shape[1] != 1 + kmax:
+            h = h.gather(1, pick[:, :, None].expand(n, 1 + kmax, d))
+        pooled = h[:, 0].reshape(-1).cpu().numpy().astype(np.float32)
+        if kmax == 0:
+            return np.zeros(0, np.float32), pooled
+        s = F.layer_norm(h[:, 1:], (d,), w["scorer.0.weight"], w["scorer.0.bias"], 1e-5)
+        s = F.gelu(s @ w["scorer.1.weight"].T + w["scorer.1.bias"])
+        lg = (s @ w["scorer.3.weight"].T + w["scorer.3.bias"]).reshape(n, kmax).cpu().numpy()
+        live = np.arange(kmax)[None, :] < b.marker_count.astype(np.int64)[:, None]
+        return np.where(live, lg, O.LOGIT_MASKED).astype(np.float32).reshape(-1), pooled
+

@@ -306,12 +306,17 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 std::mutex g_scratch_mu;
 std::vector<float*> g_scratch_ptr;
 
-float* scratch_on_current_device() {
+float* scratch_on_current_device(hipStream_t st) {
   int dev = 0;
   hip_ok(hipGetDevice(&dev), "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (size_t(dev) >= g_scratch_ptr.size()) g_scratch_ptr.resize(size_t(dev) + 1, nullptr);
   if (!g_scratch_ptr[dev]) {
+    // The lookup is a runtime call of its own; it is not made while the caller captures a graph.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      s1::fail(s1::kConfig, "s1k_gemm_noalloc: the first call on a GPU must come before any graph capture on it "
+                            "(that call looks up the scratch array's address)");
     float* p = nullptr;
     hip_ok(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
     g_scratch_ptr[dev] = p;
@@ -343,7 +348,7 @@ int s1k_gemm_noalloc(const void* A, int lda, const void* W, int ldw, void* C, in
     if (need > kScratchFloats)
       s1::fail(s1::kConfig, "s1k_gemm_noalloc: this shape's split-K partials need " + std::to_string(need * 4) +
                                 " bytes, more than the " + std::to_string(kScratchFloats * 4) + "-byte scratch");
-    g.ws = need ? scratch_on_current_device() : nullptr;
+    g.ws = need ? scratch_on_current_device(static_cast<hipStream_t>(stream)) : nullptr;
     if (const char* e = s1::gemm_check(g)) s1::fail(s1::kConfig, e);
     s1::gemm_launch(g, static_cast<hipStream_t>(stream));
     hip_ok(hipGetLastError(), "s1k_gemm_noalloc launch");

@@ -115,7 +115,6 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "fuseln") s.fuseln = flag();
     else if (key == "graphs") s.graphs = flag();
     else if (key == "dtype") s.f16 = one_of({"bf16", "f16"}) == "f16";
-    else if (key == "check_fault") s.check_fault = one_of({"fuserope", "fusegeglu", "fuseln"});
     else fail(kConfig, "hip settings: unknown setting `" + key + "` in `" + spec + "`");
     if (j == spec.size()) break;
   }
@@ -146,12 +145,33 @@ struct Model::Acts {
 Model::Model(const SafeTensors& st, const std::string& enc_json, const std::string& agent_json,
              const std::string& settings, int dev)
     : device(dev) {
+  // A load that fails part way gives back what it had already allocated (the destructor does not
+  // run for a constructor that throws).
+  try {
+    init(st, enc_json, agent_json, settings);
+  } catch (...) {
+    teardown();
+    throw;
+  }
+}
+
+void Model::init(const SafeTensors& st, const std::string& enc_json, const std::string& agent_json,
+                 const std::string& settings) {
+  const int dev = device;
   cfg = parse_model_config(enc_json, agent_json);
   set = Settings::parse(settings);
   // headprune prunes the last head layer; with no head layers the scorer reads the encoder's
   // stream whole, as head_forward's loop then leaves it (lib.rs:1726-1765).
   if (cfg.head_layers == 0) set.headprune = false;
   elem = set.f16 ? ELEM_F16 : ELEM_BF16;
+  // The forwards `warm` runs at load (warm_buckets) are checked before any device work.
+  if (std::any_of(set.warm.begin(), set.warm.end(), [](size_t n) { return n > 0; }))
+    for (size_t len : set.buckets) {
+      if (len < 3) fail(kConfig, "hip settings: warm needs buckets of at least 3 tokens");
+      if (len > size_t(cfg.max_pos))
+        fail(kConfig, "hip settings: warm bucket " + std::to_string(len) + " is longer than max_position_embeddings (" +
+                          std::to_string(cfg.max_pos) + ")");
+    }
   if (cfg.head_dim() != 64)
     fail(kConfig, "the HIP kernels need a head dim of 64; this encoder has " + std::to_string(cfg.head_dim()));
   if (cfg.d % 128 != 0 || cfg.d > kMaxHidden)
@@ -278,9 +298,15 @@ Model::Model(const SafeTensors& st, const std::string& enc_json, const std::stri
   // ---- load-time checks of the fused kernels (lib.rs:319-362): decided here, never in a request.
   // A kernel that does not match its unfused twin is turned off for this load, with one line on
   // stderr, and the forward runs the unfused kernels instead.
+  // Tests plant a wrong value in one check through the environment (SYS1HIP_CHECK_FAULT=fuserope,
+  // fusegeglu or fuseln), never through the settings string that production passes.
+  const char* fault_env = std::getenv("SYS1HIP_CHECK_FAULT");
+  const std::string check_fault = fault_env ? fault_env : "";
+  if (!check_fault.empty() && check_fault != "fuserope" && check_fault != "fusegeglu" && check_fault != "fuseln")
+    fail(kConfig, "SYS1HIP_CHECK_FAULT=" + check_fault + " is not one of fuserope, fusegeglu, fuseln");
   auto decide = [&](bool& on, const char* nm, const char* instead, auto&& check) {
     if (!on) return;
-    const std::string why = check(set.check_fault == nm);
+    const std::string why = check(check_fault == nm);
     if (why.empty()) return;
     on = false;
     std::fprintf(stderr, "libsys1hip: %s is off for this load, %s run instead: %s\n", nm, instead, why.c_str());
@@ -355,8 +381,10 @@ Model::Model(const SafeTensors& st, const std::string& enc_json, const std::stri
   warm_buckets();
 }
 
-Model::~Model() {
-  // Teardown: errors here have nowhere to go, the process keeps running.
+Model::~Model() { teardown(); }
+
+void Model::teardown() {
+  // Errors here have nowhere to go, the process keeps running.
   if (stream) (void)hipStreamSynchronize(stream);
   drop_graphs();
   for (auto& r : pending) {
@@ -371,6 +399,12 @@ Model::~Model() {
   if (hmeta) (void)hipHostFree(hmeta);
   if (hout) (void)hipHostFree(hout);
   if (stream) (void)hipStreamDestroy(stream);
+  pending.clear();
+  event_pool.clear();
+  wmem = rmem = amem = nullptr;
+  dmeta = nullptr;
+  hmeta = hout = nullptr;
+  stream = nullptr;
 }
 
 // One forward per (bucket length, warm row count) at load (MlxBackend::warm_buckets,

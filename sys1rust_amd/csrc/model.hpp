@@ -41,7 +41,6 @@ struct Settings {
   bool fuseln = true;      // a split-K Wo / Wo2 finishes in the kernel of the LayerNorm after it
   bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
   bool f16 = false;        // dtype=f16: weights and activations in f16 (the checkpoint's type), not bf16
-  std::string check_fault;  // tests only: perturb this fused kernel's output in its load check
   static Settings parse(const std::string& spec);
 };
 
@@ -170,6 +169,9 @@ struct Model {
 
  private:
   struct Acts;
+  void init(const SafeTensors& st, const std::string& enc_json, const std::string& agent_json,
+            const std::string& settings);
+  void teardown();
   Acts arena(const Plan& p);
   void upload(const Plan& p);
   // Enqueues the encoder; with fold_last, the last layer's Wo2 may leave its split-K partials in

@@ -349,6 +349,43 @@ std::string check_fuseln(int elem, int d, float eps, hipStream_t st, bool fault)
       std::snprintf(buf_msg, sizeof buf_msg, "head end: scorer row %d, column %d differs", int(i / N), int(i % N));
       return buf_msg;
     }
+  if (!split) return "";
+  // The pruned head's norm2: each output row's residual is a row of a longer stream, picked through
+  // a row index (hsrc / hrows), with the out_proj bias and the LayerNorm's bias. Against the gather
+  // of those rows, the GEMM's own split-K reduce with the bias and layernorm_launch with the bias.
+  const int Hrows = 2 * M;
+  std::vector<float> hs(size_t(Hrows) * N);
+  std::vector<int> hr(M);
+  for (size_t i = 0; i < hs.size(); ++i) hs[i] = uniform(38, i, 1.7f);
+  for (int r = 0; r < M; ++r) hr[r] = (r * 37 + 11) % Hrows;  // distinct rows, out of order
+  Dev dhs(hs.size() * 4), dhr(size_t(M) * 4), hA(size_t(M) * N * 4), hB(size_t(M) * N * 4);
+  Dev yA(size_t(M) * N * 2), yB(size_t(M) * N * 2);
+  up(dhs.p, hs, st);
+  up(dhr.p, hr, st);
+  GemmArgs gp2 = g;
+  gp2.C = hB.p;
+  gp2.bias = dlb.as<float>();
+  gemm_launch_partials(gp2, st);
+  splitk_resid_ln_launch(ws.as<float>(), gp2.splits, dlb.as<float>(), hA.as<float>(), dlw1.as<float>(), 1e-5f, M, N,
+                         yA.as<uint16_t>(), st, elem, dlb.as<float>(), dhs.as<float>(), dhr.as<int>());
+  gather_f32_launch(dhs.as<float>(), dhr.as<int>(), M, N, hB.as<float>(), st);
+  gemm_launch(gp2, st);
+  layernorm_launch(hB.as<float>(), nullptr, dlw1.as<float>(), dlb.as<float>(), 1e-5f, M, N, yB.as<uint16_t>(), nullptr,
+                   nullptr, nullptr, nullptr, st, elem);
+  hc(hipGetLastError(), "launch");
+  const auto pa2 = down<uint32_t>(hA.p, size_t(M) * N, st), pb2 = down<uint32_t>(hB.p, size_t(M) * N, st);
+  for (size_t i = 0; i < pa2.size(); ++i)
+    if (pa2[i] != pb2[i]) {
+      std::snprintf(buf_msg, sizeof buf_msg, "picked rows: h row %d, column %d differs", int(i / N), int(i % N));
+      return buf_msg;
+    }
+  const auto ua = down<uint16_t>(yA.p, size_t(M) * N, st), ub = down<uint16_t>(yB.p, size_t(M) * N, st);
+  for (size_t i = 0; i < ua.size(); ++i)
+    if (ua[i] != ub[i]) {
+      std::snprintf(buf_msg, sizeof buf_msg, "picked rows: norm2 output row %d, column %d differs", int(i / N),
+                    int(i % N));
+      return buf_msg;
+    }
   return "";
 }
 

@@ -102,6 +102,33 @@ class ActHead:
     def from_weights(cls, w: dict) -> "ActHead":
         return cls(w["act_head.0.weight"], w["act_head.0.bias"], w["act_head.2.weight"], w["act_head.2.bias"])
 
+    @classmethod
+    def from_safetensors(cls, st: bytes) -> "ActHead":
+        """The act_head tensors of a safetensors image (F32, F16 or BF16), read as laya-core reads
+        them at load (decode.rs:130-136)."""
+        import json
+        import struct
+
+        n = struct.unpack("<Q", st[:8])[0]
+        header = json.loads(st[8:8 + n])
+        w = {}
+        for name in ("act_head.0.weight", "act_head.0.bias", "act_head.2.weight", "act_head.2.bias"):
+            if name not in header:
+                raise ValueError(f"checkpoint has no {name}")
+            e = header[name]
+            a, z = (8 + n + o for o in e["data_offsets"])
+            raw = st[a:z]
+            if e["dtype"] == "F32":
+                v = np.frombuffer(raw, np.float32)
+            elif e["dtype"] == "F16":
+                v = np.frombuffer(raw, np.float16).astype(np.float32)
+            elif e["dtype"] == "BF16":
+                v = (np.frombuffer(raw, np.uint16).astype(np.uint32) << 16).view(np.float32)
+            else:
+                raise ValueError(f"{name}: dtype {e['dtype']} is not F32, F16 or BF16")
+            w[name] = v.reshape(e["shape"])
+        return cls.from_weights(w)
+
     def pooled_width(self) -> int:
         return self.d_in - 4
 

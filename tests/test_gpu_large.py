@@ -5,8 +5,9 @@ restatement (oracle/torch_ref.py) on the GPU; tests/test_oracle.py pins that res
 numpy oracle and the golden fixtures. The first test re-pins it on the GPU against the numpy
 oracle at a size the latter finishes in seconds.
 
-Gates as elsewhere: identical choice per choice question, probabilities and act_probability within
-5e-3, hidden states within 2e-2 relative, on every row of the sweep. Properties at full size: rows
+Gates as elsewhere: identical decisions per question (choice, score level, noul side),
+probabilities and act_probability within 5e-3, logits within 0.15, hidden states within 2e-2
+relative, on every row of the sweep. Properties at full size: rows
 are independent, so a subset of the packed batch run alone must give the same answers, and every
 output is finite. The model runs sys1rust's production settings (DEFAULT_TUNING).
 """
@@ -23,7 +24,7 @@ from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
 from sys1rust_amd.decode import ActHead
 from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, Batch, workload
 
-from gates import FUSED, HIDDEN_REL_GATE, check_act, check_answers, hidden_rel, say
+from gates import FUSED, HIDDEN_REL_GATE, check_act, check_answers, check_logits, hidden_rel, say
 
 pytestmark = pytest.mark.gpu
 
@@ -66,6 +67,7 @@ def test_state8192_single_question(big):
     assert rel <= HIDDEN_REL_GATE
     lg_ref, pl_ref = t.forward(b, ref)
     check_answers(out.logits, lg_ref, b, "state8192_1q")
+    check_logits(out.logits, lg_ref, b, "state8192_1q")
     check_act(out.logits, out.pooled, lg_ref, pl_ref, b, ActHead.from_weights(t.o.w), "state8192_1q")
     pr = float(np.linalg.norm(out.pooled - pl_ref) / np.linalg.norm(pl_ref))
     say(f"state8192_1q: pooled rel {pr:.3e}")
@@ -120,6 +122,7 @@ def test_sweep64_packed_batch_every_row(big):
         lg_ref, pl_ref = t.forward(sub, ref)
         lg, pl = lg_all[rows].reshape(-1), pl_all[rows].reshape(-1)
         check_answers(lg, lg_ref, sub, f"sweep64 rows {rows[0]}..")
+        check_logits(lg, lg_ref, sub, f"sweep64 rows {rows[0]}..")
         check_act(lg, pl, lg_ref, pl_ref, sub, act, f"sweep64 rows {rows[0]}..")
     say(f"sweep64: every row checked; worst hidden rel {worst:.3e}")
     # Rows are independent: the shortest, the longest and one row of each type run alone answer

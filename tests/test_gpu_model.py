@@ -87,7 +87,7 @@ def test_decision_head_depths(small_model, head_layers):
     outs = []
     for settings in (DEFAULT_TUNING, DEFAULT_TUNING + ",headprune=0", DEFAULT_TUNING + ",fuseln=0"):
         m = HipBackend(st, json.dumps(cfg), json.dumps(ag), settings=settings)
-        outs.append(gate_model(m, b, ref, lg_ref, pl_ref, act, f"head_layers={head_layers} {settings}"))
+        outs.append(gate_model(m, b, ref, lg_ref, pl_ref, act, f"head_layers={head_layers} {settings}")[0])
         m.close()
     assert np.array_equal(outs[0].logits, outs[2].logits) and np.array_equal(outs[0].pooled, outs[2].pooled)
 
@@ -180,7 +180,7 @@ def test_settings_variants_match_oracle(small_model, small_ref, settings):
     m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=settings)
     want = [k for k in FUSED if f"{k}=0" not in settings and (k != "fuserope" or "fuserope" in settings)]
     assert m.active_kernels() == want, (m.active_kernels(), want)
-    out = gate_model(m, b, ref, lg_ref, pl_ref, act, f"small {settings}")
+    out, _ = gate_model(m, b, ref, lg_ref, pl_ref, act, f"small {settings}")
     if "mask=bool" in settings or settings.endswith(",fuseln=0"):
         base = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=DEFAULT_TUNING)
         o1 = base.forward(b)
@@ -191,22 +191,24 @@ def test_settings_variants_match_oracle(small_model, small_ref, settings):
 
 
 @pytest.mark.parametrize("kernel", FUSED)
-def test_load_check_turns_off_a_wrong_kernel(small_model, small_ref, kernel, capfd):
+def test_load_check_turns_off_a_wrong_kernel(small_model, small_ref, kernel, capfd, monkeypatch):
     """The load-time check (lib.rs:319-362): a fused kernel whose output does not match its unfused
     twin is turned off for the load with one stderr line, is missing from active_kernels, and the
     forward runs the unfused kernels, which pass the gates and give the bits of a model loaded
-    with that setting off. check_fault perturbs one value of the fused output inside the check
-    (a wrong result, not a fault)."""
+    with that setting off. SYS1HIP_CHECK_FAULT (read at create, tests only) perturbs one value of
+    the fused output inside the check (a wrong result, not a fault)."""
     cfg, agent, st, b, z = small_model
     o, ref, lg_ref, pl_ref, act = small_ref
     say(f"load check with a wrong {kernel}")
     capfd.readouterr()
-    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=f"{DEFAULT_TUNING},check_fault={kernel}")
+    monkeypatch.setenv("SYS1HIP_CHECK_FAULT", kernel)
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=DEFAULT_TUNING)
+    monkeypatch.delenv("SYS1HIP_CHECK_FAULT")
     err = capfd.readouterr().err
     assert f"libsys1hip: {kernel} is off for this load" in err, err
     assert err.count("libsys1hip:") == 1, err
     assert m.active_kernels() == [k for k in FUSED if k != kernel]
-    out = gate_model(m, b, ref, lg_ref, pl_ref, act, f"fallback {kernel}")
+    out, _ = gate_model(m, b, ref, lg_ref, pl_ref, act, f"fallback {kernel}")
     off = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=f"{DEFAULT_TUNING},{kernel}=0")
     o2 = off.forward(b)
     assert np.array_equal(out.logits, o2.logits) and np.array_equal(out.pooled, o2.pooled)
@@ -322,7 +324,7 @@ def test_f16_matches_oracle_closer_than_bf16(small_model, small_ref):
     assert r16 <= HIDDEN_REL_GATE and r16 <= 0.2 * rbf, (r16, rbf)
     for name in ("fusegeglu=0,fuseln=0", DEFAULT_TUNING):
         mm = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f16," + name)
-        out = gate_model(mm, b, ref, lg_ref, pl_ref, act, f"f16 {name}")
+        out, _ = gate_model(mm, b, ref, lg_ref, pl_ref, act, f"f16 {name}")
         p16 = float(np.linalg.norm(out.pooled - pl_ref) / np.linalg.norm(pl_ref))
         pbf = float(np.linalg.norm(mbf.forward(b).pooled - pl_ref) / np.linalg.norm(pl_ref))
         say(f"f16 {name}: pooled rel {p16:.3e} (bf16 {pbf:.3e})")

@@ -108,6 +108,32 @@ def test_torch_restatement_matches_oracle_and_golden(case):
     assert float(np.abs(lt - lo).max()) < 1e-5
 
 
+@pytest.mark.parametrize("headprune", [True, False])
+@pytest.mark.parametrize("case", ["golden_small", "golden_large"])
+def test_batched_torch_restatement_matches_oracle(case, headprune):
+    """TorchOracle.forward_batched, the CPU baseline's forward (the whole padded batch per layer,
+    torch's fused layer_norm / gelu / attention, the pruned last head layer), gives the oracle's
+    logits and pooled rows to float32 rounding, with and without head pruning."""
+    import torch
+
+    from oracle.torch_ref import TorchOracle
+
+    z, cfg, agent, b, st = load_case(case)
+    o = O.Oracle(st, cfg, agent)
+    lo, po = o.forward(b)
+    with torch.no_grad():
+        lt, pt = TorchOracle(o, "cpu").forward_batched(b, headprune=headprune)
+    assert lt.shape == lo.shape and pt.shape == po.shape
+    assert float(np.abs(lt - lo).max()) < 1e-4, float(np.abs(lt - lo).max())
+    assert float(np.linalg.norm(pt - po) / np.linalg.norm(po)) < 1e-5
+    assert np.array_equal(lt == O.LOGIT_MASKED, lo == O.LOGIT_MASKED)
+    # a planted mistake in the batched path is visible at these tolerances: the window one wider
+    o.window += 1
+    with torch.no_grad():
+        lw, pw = TorchOracle(o, "cpu").forward_batched(b, headprune=headprune)
+    assert float(np.linalg.norm(pw - po) / np.linalg.norm(po)) > 1e-4
+
+
 @pytest.mark.parametrize("mistake", ["window+1", "theta_swap", "geglu_order", "head_scale", "drop_out_proj_bias",
                                      "emb_norm_weight_dropped", "rope_traditional"])
 def test_planted_mistakes_fail_the_golden_check(small, mistake, monkeypatch):

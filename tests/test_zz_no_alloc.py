@@ -50,3 +50,39 @@ def test_noalloc_gemm_matches_allocating_gemm(epi, act, bias):
             ref = ref + base
         err = (c2.float() - ref).abs().max().item()
         assert err <= 2e-2 * max(1.0, ref.abs().max().item()), err
+
+
+def test_noalloc_gemm_under_graph_capture():
+    """The captured call replays the eager call's bits: a split-K product (its partials in the
+    static scratch) captured in a graph after one eager call on the GPU, replayed several times
+    with eager work and new inputs between the replays, each replay checked against s1k_gemm."""
+    import torch
+
+    L = _lib.lib()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    M, N, K = 128, 1024, 1024
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    W = (0.02 * torch.randn(N, K, device="cuda", generator=g)).to(torch.bfloat16)
+    bias = torch.randn(N, device="cuda", generator=g)
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    want = torch.zeros_like(out)
+
+    def call(fn, C_, st):
+        return fn(C.c_void_p(A.data_ptr()), K, C.c_void_p(W.data_ptr()), K, C.c_void_p(C_.data_ptr()), N,
+                  C.c_void_p(bias.data_ptr()), M, N, K, 0, 2, C.c_void_p(st))
+
+    _run(L.s1k_gemm_noalloc, A, W, out, bias, M, N, K, 0, 2)  # first call on this GPU: outside capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = call(L.s1k_gemm_noalloc, out, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    for i in range(4):
+        print(f"noalloc graph: replay {i}", flush=True)
+        out.zero_()
+        if i:
+            A.copy_(torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _run(L.s1k_gemm, A, W, want, bias, M, N, K, 0, 2)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), i
