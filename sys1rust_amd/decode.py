@@ -7,13 +7,15 @@ temperature of the (qtype, k) bucket (decode.rs:16-86); p = softmax in f64; choi
 the first maximum winning (decode.rs:335-338), score = sum_i i * p_i, noul = p[1];
 confidence = 1 - H(p) / ln k (decode.rs:88-94) on choice and score, max(p_yes, p_no) on noul;
 answer_confidence = the probability of the reported answer. With an action head,
-act_probability = ActHead.probs(pooled[r], act_features(logits[r], k))[0] (decode.rs:319-331).
+act_probability = ActHead.probs(pooled[r], act_features(logits[r], k))[0] (decode.rs:319-331), the
+head's rows evaluated together.
 """
 from __future__ import annotations
 
 import math
 
 import numpy as np
+from scipy.special import erf as _erf
 
 TEMP_MIN, TEMP_MAX = 0.5, 5.0
 QTYPE_NAMES = ["choice", "score", "noul"]
@@ -58,10 +60,8 @@ def confidence_from_probs(p, k: int) -> float:
 
 def gelu_f64(x):
     """decode.rs:111-115: exact-erf GELU evaluated in f64, returned as f32."""
-    from scipy.special import erf
-
     xf = np.asarray(x, dtype=np.float64)
-    return (0.5 * xf * (1.0 + erf(xf / math.sqrt(2.0)))).astype(np.float32)
+    return (0.5 * xf * (1.0 + _erf(xf / math.sqrt(2.0)))).astype(np.float32)
 
 
 def softmax_f32(z) -> np.ndarray:
@@ -81,6 +81,20 @@ def act_features(logits_row, marker_count: int) -> np.ndarray:
     top1 = srt[0] if srt.size else np.float32(0)
     top2 = srt[1] if srt.size > 1 else np.float32(0)
     return np.array([top1, top1 - top2, ent, k / np.float32(255.0)], dtype=np.float32)
+
+
+def act_features_rows(logits, kmax: int, marker_count) -> np.ndarray:
+    """act_features of every row of a [n * kmax] logits buffer at once -> [n, 4]."""
+    n = len(marker_count)
+    z = np.asarray(logits, dtype=np.float32)[: n * kmax].reshape(n, kmax)
+    e = np.exp(z - z.max(axis=1, keepdims=True)).astype(np.float32)
+    p = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    k = np.maximum(np.asarray(marker_count, dtype=np.int64), 2).astype(np.float32)
+    ent = (-(p * np.log(np.maximum(p, np.float32(1e-9)))).sum(axis=1, dtype=np.float32) / np.log(k)).astype(np.float32)
+    srt = -np.sort(-p, axis=1)
+    top1 = srt[:, 0] if kmax else np.zeros(n, np.float32)
+    top2 = srt[:, 1] if kmax > 1 else np.zeros(n, np.float32)
+    return np.stack([top1, top1 - top2, ent, k / np.float32(255.0)], axis=1).astype(np.float32)
 
 
 class ActHead:
@@ -133,10 +147,15 @@ class ActHead:
         return self.d_in - 4
 
     def probs(self, pooled, feats) -> np.ndarray:
-        x = np.concatenate([np.asarray(pooled, dtype=np.float32), np.asarray(feats, dtype=np.float32)])
-        h = gelu_f64((self.w0 @ x + self.b0).astype(np.float32))
-        out = (self.w2 @ h + self.b2).astype(np.float32)
-        return softmax_f32(out)
+        return self.probs_rows(np.asarray(pooled, dtype=np.float32)[None], np.asarray(feats, dtype=np.float32)[None])[0]
+
+    def probs_rows(self, pooled, feats) -> np.ndarray:
+        """probs() of every row at once: pooled [n, d], feats [n, 4] -> [n, n_act]."""
+        x = np.concatenate([np.asarray(pooled, dtype=np.float32), np.asarray(feats, dtype=np.float32)], axis=1)
+        h = gelu_f64((x @ self.w0.T + self.b0).astype(np.float32))
+        out = (h @ self.w2.T + self.b2).astype(np.float32)
+        e = np.exp(out - out.max(axis=1, keepdims=True)).astype(np.float32)
+        return (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
 
 
 def round_dp(x: float, n: int = 4) -> float:
@@ -147,6 +166,12 @@ def decode_answers(logits: np.ndarray, kmax: int, marker_count, qtype, temperatu
                    temperature_by_options: dict | None = None, pooled=None, act_head: ActHead | None = None):
     by_type = [clamp_temperature(t) for t in temperature]
     by_opt = {k: clamp_temperature(v) for k, v in (temperature_by_options or {}).items()}
+    act = None
+    if act_head is not None:
+        # The action head of every row in one product (the rows are independent).
+        n, d = len(qtype), act_head.pooled_width()
+        feats = act_features_rows(logits, kmax, marker_count)
+        act = act_head.probs_rows(np.asarray(pooled, dtype=np.float32)[: n * d].reshape(n, d), feats)
     out = []
     for r in range(len(qtype)):
         k = int(marker_count[r])
@@ -171,9 +196,7 @@ def decode_answers(logits: np.ndarray, kmax: int, marker_count, qtype, temperatu
             p1 = float(p[1]) if k > 1 else 0.0
             ans["noul"] = p1
             ans["confidence"] = ans["answer_confidence"] = max(p1, 1.0 - p1)
-        if act_head is not None:
-            d = act_head.pooled_width()
-            row = logits[r * kmax: (r + 1) * kmax]
-            ans["act_probability"] = float(act_head.probs(pooled[r * d: (r + 1) * d], act_features(row, k))[0])
+        if act is not None:
+            ans["act_probability"] = float(act[r, 0])
         out.append(ans)
     return out
