@@ -77,8 +77,8 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 // as one 8-byte (bf16) or 16-byte (f32) access after a packed conversion. !TR: D = A . W^T, a
 // lane holds one column and four consecutive rows per g; only the transposed v output of the
 // q|k|v epilogue ([H, 64, ldv], rows = tokens contiguous) wants that.
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0, int n0, int kt0, int NK, int split) {
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR, int KG>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0, int n0, int kt0, int NK, int split) {
   constexpr int NW = WM * WN;                // waves; each owns a TM x TN sub-tile
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;  // 32 x 32 MFMA fragments per wave
@@ -94,7 +94,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
   static_assert(LPW * NW == AG + WG, "load groups must split evenly over the waves");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt range");
 
-  const int tid = threadIdx.x;
+  // KG > 1 (k-groups): the workgroup holds KG groups of NW waves; group k runs k-tiles
+  // [kt0 + k NK / KG, kt0 + (k + 1) NK / KG) on stage buffers of its own (NK divides by KG, so
+  // every group passes the same barriers), and group 0 adds the other groups' accumulators, in
+  // group order, from LDS and runs the epilogue alone. A short GEMM's chain of dependent k-tiles
+  // is then KG times shorter on the same tiles.
+  const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6) / NW : 0;
+  const int tid = threadIdx.x - grp * NW * 64;
+  char* const smem = smem0 + grp * STAGES * STAGE_BYTES;
+  if constexpr (KG > 1) {
+    kt0 += grp * (NK / KG);
+    NK /= KG;
+  }
   const int lane = tid & 63;
   // Wave-uniform, so everything derived from it (load row groups, LDS destinations) is scalar.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -182,6 +193,42 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
     }
   }
 
+  if constexpr (KG > 1) {
+    // Groups 1.. leave their accumulators in their own stage buffers, in register order (float4
+    // e4 of fragment (i, j) of wave w at ((w FM + i) FN + j) 4 + e4, 64 lanes apart), and end;
+    // waves that have ended take no part in the barriers that follow.
+    static_assert(BM * BN * 4 <= STAGES * STAGE_BYTES, "a group's partial tile must fit its stage buffers");
+    __syncthreads();  // every group is done reading its stage buffers
+    if (grp > 0) {
+      float4* dst = reinterpret_cast<float4*>(smem);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4)
+            dst[(((wave * FM + i) * FN + j) * 4 + e4) * 64 + lane] =
+                make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int gg = 1; gg < KG; ++gg) {
+      const float4* src = reinterpret_cast<const float4*>(smem0 + gg * STAGES * STAGE_BYTES);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const float4 v = src[(((wave * FM + i) * FN + j) * 4 + e4) * 64 + lane];
+            acc[i][j][4 * e4] += v.x;
+            acc[i][j][4 * e4 + 1] += v.y;
+            acc[i][j][4 * e4 + 2] += v.z;
+            acc[i][j][4 * e4 + 3] += v.w;
+          }
+    }
+  }
   const int l32 = lane & 31, h = lane >> 5;
   constexpr int NT = NW * 64;
   // bf16 results leave through LDS: after the k-loop the stage buffers are free, each wave
@@ -481,13 +528,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int m0,
   }
 }
 
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG>
+__global__ __launch_bounds__(WM * WN * 64 * KG) void gemm_kernel(GemmArgs g) {
   // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of BK * 2 bytes. The 16-byte chunk c
   // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
   // consecutive rows, the same k; 64 banks of 4 bytes) then hit 16 distinct 16-byte bank groups
   // without padding, which the direct loads (whole 1 KiB runs) could not write.
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * (BM + BN) * BK * 2];
+  __shared__ __attribute__((aligned(1024))) char smem[KG * STAGES * (BM + BN) * BK * 2];
 
   // Tile order: each XCD takes a contiguous run of logical tiles (xcd_remap), and the run walks
   // groups of GM row tiles across all column tiles, GM fastest. The workgroups an XCD holds at
@@ -512,18 +559,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 
   if constexpr (EPI == EPI_ROPE) {
     if (n0 >= 2 * g.rope_d) {
-      gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, false>(g, smem, m0, n0, kt0, NK, split);
+      gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, false, KG>(g, smem, m0, n0, kt0, NK, split);
       return;
     }
   }
-  gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, true>(g, smem, m0, n0, kt0, NK, split);
+  gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, true, KG>(g, smem, m0, n0, kt0, NK, split);
 }
 
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG = 1>
 void launch_t(const GemmArgs& g, hipStream_t st) {
   const int mt = (g.M + BM - 1) / BM, nt = g.N / BN;
-  hipLaunchKernelGGL((gemm_kernel<E, BM, BN, BK, STAGES, WM, WN, EPI>), dim3(mt * nt, g.splits), dim3(WM * WN * 64), 0,
-                     st, g);
+  hipLaunchKernelGGL((gemm_kernel<E, BM, BN, BK, STAGES, WM, WN, EPI, KG>), dim3(mt * nt, g.splits),
+                     dim3(WM * WN * 64 * KG), 0, st, g);
 }
 
 // Tile configurations, chosen from the number of tiles the GEMM has (the GPU holds two
@@ -561,18 +608,24 @@ inline int tile_m_of(int M, int N) {
 template <class E, int EPI>
 void launch_te(const GemmArgs& g, hipStream_t st) {
   switch (tile_cfg(g.M, g.N)) {
-    case TC_SMALL:
+    case TC_SMALL: {
       // Four k-tiles in flight when the launch fits one workgroup per CU (96 KiB of LDS each):
       // deeper prefetch for the weight stream. Past one workgroup per CU, 128 x 128 tiles with
       // three stages while they still fit about one per CU (up to 320 of them), else 64-row
       // tiles with three stages, two workgroups per CU. In a one-request forward at 565 tokens
       // (weights cold in HBM) the wide GeGLU product (N = 2I, 369 64-row tiles) drops from 17.6
       // to 14.9 µs per launch with the 128 x 128 tiles; two stages there lose to 64-row tiles.
-      // The k-loop order is the same for every tile, so the results are the same bits. The q|k|v
-      // product takes 64 x 64 tiles while they fit one workgroup per CU (a third fewer bytes per
-      // k-tile, twice the workgroups): at 174 tokens 13.0 -> 12.2 µs per launch (the GeGLU
-      // product lost 2% that way).
-      if (EPI == EPI_ROPE && (long long)((g.M + 63) / 64) * (g.N / 64) * g.splits <= 256)
+      // Except for the k-groups below, the k-loop order is the same for every tile, so the results
+      // are the same bits. The q|k|v product takes 64 x 64 tiles while they fit one workgroup per
+      // CU (a third fewer bytes per k-tile, twice the workgroups): at 174 tokens 13.0 -> 12.2 µs
+      // per launch (the GeGLU product lost 2% that way). A GEMM with a 16-bit epilogue whose
+      // 64 x 64 tiles fit one workgroup per CU runs them in two k-groups of 4 waves (8 k-tiles
+      // each where there were 16): at 174 tokens q|k|v 9.9 -> 8.9 µs and GeGLU 9.8 -> 8.2 µs
+      // (GeGLU on twice the workgroups of its 64 x 128 tiles), weights cold in HBM.
+      constexpr bool KGOK = EPI != EPI_RESID && EPI != EPI_F32;
+      if (KGOK && g.splits == 1 && (g.K / BK) % 2 == 0 && (long long)((g.M + 63) / 64) * (g.N / 64) <= 256)
+        launch_t<E, 64, 64, 64, 4, 2, 1, EPI, KGOK ? 2 : 1>(g, st);
+      else if (EPI == EPI_ROPE && (long long)((g.M + 63) / 64) * (g.N / 64) * g.splits <= 256)
         launch_t<E, 64, 64, 64, 4, 2, 1, EPI>(g, st);
       else if ((long long)((g.M + 63) / 64) * (g.N / 128) * g.splits <= 256)
         launch_t<E, 64, 128, 64, 4, 2, 2, EPI>(g, st);
@@ -581,6 +634,7 @@ void launch_te(const GemmArgs& g, hipStream_t st) {
       else
         launch_t<E, 64, 128, 64, 3, 2, 2, EPI>(g, st);
       break;
+    }
     case TC_WIDE: launch_t<E, 192, 128, 64, 2, 2, 2, EPI>(g, st); break;
     case TC_MID: launch_t<E, 64, 128, 64, 2, 2, 2, EPI>(g, st); break;
   }
