@@ -90,8 +90,13 @@ int s1_forward(s1_model* m, uint32_t n, uint32_t len, uint32_t kmax, const uint3
                const uint64_t* marker_count, const uint32_t* qtype, float* logits_out,
                float* pooled_out);
 
-/* Backend::encoder_hidden (lib.rs:1869-1878): the encoder's last_hidden_state as f32
- * [n*len*d]. Positions with attention_mask 0 are not computed and are written as 0.0. */
+/* Backend::encoder_hidden (lib.rs:1864-1878): the encoder's last_hidden_state as f32
+ * [n*len*d], computed at every position including padding: the encoder runs the padded layout
+ * (every position a row, RoPE position = index in the row), and a padding position attends as
+ * the reference's masks let it, which the settings mask / windowed / dense_upto / band / fuserope
+ * decide as they decide MlxBackend's path for this len (lib.rs:1241-1310). The batch checks are
+ * s1_forward's; kmax, marker_pos, marker_count and qtype are not read; len must be at most
+ * max_position_embeddings. */
 int s1_encoder_hidden(s1_model* m, uint32_t n, uint32_t len, uint32_t kmax,
                       const uint32_t* input_ids, const uint32_t* attention_mask,
                       const uint64_t* seq_lens, const uint32_t* marker_pos,

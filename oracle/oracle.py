@@ -9,8 +9,10 @@ It follows MlxBackend op for op in the padded layout that `encoder_hidden` uses
 
   encode        lib.rs:1525-1693  h = LN(tok_emb[ids]); 28 x {attn_norm (not layer 0), Wqkv,
                                   split + RoPE (split_rope.rs:44-54), SDPA with the additive
-                                  -1e4 pad mask (global, lib.rs:1227-1235) or pad + |i-j| <= W
-                                  window mask (local, lib.rs:1399-1417), h += att Wo^T,
+                                  -1e4 pad mask (global, lib.rs:1227-1235) or, on local layers,
+                                  the path attn_ctx picks (lib.rs:1241-1310): pad + |i-j| <= W
+                                  window masks (dense), chunked or banded windows, additive or
+                                  boolean masks (local_attention), h += att Wo^T,
                                   mlp_norm, Wi, GeGLU (lib.rs:494-510), h += act Wo2^T};
                                   final_norm
   head_forward  lib.rs:1698-1765  h + type_emb[qtype]; pre-norm layers with biases, 16 heads,
@@ -26,7 +28,8 @@ with the cosine and sine of that f32 angle taken in double.
 Pinned by tests/test_oracle.py against tests/golden/ fixtures written by transformers'
 ModernBertModel and torch's TransformerEncoderLayer (an independent implementation of the same
 model), against closed forms (LayerNorm, GELU, the RoPE rotation) and against brute-force
-invariants (row independence, padding invariance, window locality).
+invariants (row independence, padding invariance, window locality); the mask paths against the
+reference's chunk-table fixture (lib.rs:2175-2247) and a slot-by-slot brute force.
 """
 from __future__ import annotations
 
@@ -117,9 +120,109 @@ def sdpa(q, k, v, scale: float, mask) -> np.ndarray:
     return np.matmul(p, v).astype(np.float32)
 
 
+# ---- local attention as the reference chooses it per batch length (lib.rs:1241-1310, 1428-1475)
+MASK_KEYS = ("mask", "windowed", "dense_upto", "band", "fuserope")
+
+
+def mask_options(settings: str = "") -> dict:
+    """The Knobs keys (lib.rs:196-256) that choose the attention masks, from a settings string:
+    mask (additive | bool), windowed (flag, default on), dense_upto (None: 4 * window), band
+    (0: off) and fuserope (band needs it, lib.rs:330-361). Other keys are ignored."""
+    o = {"bool_mask": False, "windowed": True, "dense_upto": None, "band": 0, "fuserope": False}
+    for kv in filter(None, settings.split(",")):
+        key, _, val = kv.partition("=")
+        flag = val in ("", "1")
+        if key == "mask":
+            o["bool_mask"] = val == "bool"
+        elif key == "windowed":
+            o["windowed"] = flag
+        elif key == "dense_upto":
+            o["dense_upto"] = int(val)
+        elif key == "band":
+            o["band"] = int(val)
+        elif key == "fuserope":
+            o["fuserope"] = flag
+    return o
+
+
+def band_allows(s: int) -> np.ndarray:
+    """[S, 3S] bool (lib.rs:512-523): query i of a chunk may see gathered slot j iff |S + i - j| <= S."""
+    i = np.arange(s)[:, None]
+    j = np.arange(3 * s)[None, :]
+    return np.abs(s + i - j) <= s
+
+
+def window_positions(s: int, nc: int) -> np.ndarray:
+    """[nc, 3S] int: slot j of chunk c holds position (c - 1) S + j (lib.rs:804-814, before the clamp)."""
+    return (np.arange(nc)[:, None] - 1) * s + np.arange(3 * s)[None, :]
+
+
+def window_key_valid(am: np.ndarray, s: int, nc: int) -> np.ndarray:
+    """[nc, 3S] bool for one row (lib.rs:542-557): the slot's position lies in the row and is real."""
+    pos = window_positions(s, nc)
+    inside = (pos >= 0) & (pos < am.shape[0])
+    return inside & (am[np.clip(pos, 0, am.shape[0] - 1)] == 1)
+
+
+def window_query_padded(am: np.ndarray, s: int, nc: int) -> np.ndarray:
+    """[nc, S] bool for one row (lib.rs:559-571): query c S + i is past the row or padding."""
+    padded = np.ones(nc * s, dtype=bool)
+    padded[: am.shape[0]] = am != 1
+    return padded.reshape(nc, s)
+
+
+def local_attention(q, k, v, am, scale: float, window: int, opts: dict) -> np.ndarray:
+    """Local-layer attention of one padded row, q, k, v [H, len, hd], by the path the reference
+    takes for this len (lib.rs:1241-1270): dense pad + window masks, chunked (1428-1475: queries
+    in chunks of S = window against the 3S gathered keys of chunks c - 1, c, c + 1, clamped to
+    the row), or banded (the chunked sdpa on a layout that is zero outside the row,
+    split_rope.rs:18-21). Additive masks add -1e4 per failed test; boolean masks exclude, and
+    padding queries may see every valid key (dense) or every gathered slot (chunked)."""
+    L = q.shape[1]
+    S = window
+    dense_upto = opts["dense_upto"] if opts["dense_upto"] is not None else 4 * S
+    banded = opts["band"] > 0 and opts["fuserope"] and not opts["bool_mask"] and L >= opts["band"]
+    chunked = banded or (opts["windowed"] and L > dense_upto)
+    real = am == 1
+    if not chunked:
+        idx = np.arange(L)
+        inwin = np.abs(idx[:, None] - idx[None, :]) <= S
+        if opts["bool_mask"]:  # lib.rs:1259-1264
+            allowed = (inwin | ~real[:, None]) & real[None, :]
+            mask = np.where(allowed, np.float32(0), np.float32(-np.inf)).astype(np.float32)
+        else:  # pad + window (lib.rs:1265-1266)
+            mask = (np.where(real, np.float32(0), MASK_NEG)[None, :] + np.where(inwin, np.float32(0), MASK_NEG)).astype(np.float32)
+        return sdpa(q, k, v, scale, mask[None])
+    H, hd = q.shape[0], q.shape[2]
+    nc = -(-L // S)
+    lp = nc * S
+    qp = np.zeros((H, lp, hd), np.float32)
+    qp[:, :L] = q
+    qp = qp.reshape(H, nc, S, hd)
+    pos = window_positions(S, nc)
+    idx = np.clip(pos, 0, L - 1)
+    kg, vg = k[:, idx], v[:, idx]  # [H, nc, 3S, hd]
+    if banded:
+        out = (pos < 0) | (pos >= L)
+        kg[:, out] = 0
+        vg[:, out] = 0
+    key_ok = window_key_valid(am, S, nc)
+    band = band_allows(S)
+    if opts["bool_mask"]:  # lib.rs:1279-1291
+        allowed = (key_ok[:, None, :] & band[None]) | window_query_padded(am, S, nc)[:, :, None]
+        mask = np.where(allowed, np.float32(0), np.float32(-np.inf)).astype(np.float32)
+    else:  # lib.rs:1292-1297
+        mask = (np.where(key_ok, np.float32(0), MASK_NEG)[:, None, :] + np.where(band, np.float32(0), MASK_NEG)[None]).astype(np.float32)
+    att = sdpa(qp, kg, vg, scale, mask[None])  # [H, nc, S, hd]
+    return att.reshape(H, lp, hd)[:, :L]
+
+
 class Oracle:
-    def __init__(self, st_bytes: bytes, encoder_config: dict, agent_config: dict | None = None):
+    def __init__(self, st_bytes: bytes, encoder_config: dict, agent_config: dict | None = None, settings: str = ""):
+        """settings: the backend settings string; its mask keys (mask_options) choose the local
+        attention of the padded layout, which only the padding positions tell apart."""
         self.w = load_safetensors(st_bytes)
+        self.opts = mask_options(settings)
         c = encoder_config
         self.d = c["hidden_size"]
         self.layers = c["num_hidden_layers"]
@@ -150,9 +253,9 @@ class Oracle:
         w, d, H, hd = self.w, self.d, self.heads, self.hd
         L = ids.shape[0]
         h = layer_norm(w["encoder.embeddings.tok_embeddings.weight"][ids], w["encoder.embeddings.norm.weight"], None, self.eps)
-        pad = np.where(am == 1, np.float32(0), MASK_NEG).astype(np.float32)[None, None, :]  # [1, 1, L]
-        idx = np.arange(L)
-        win = np.where(np.abs(idx[:, None] - idx[None, :]) > self.window, MASK_NEG, np.float32(0)).astype(np.float32)
+        # the key-padding mask of global layers (lib.rs:1227-1235; boolean: exclusion)
+        pad_neg = np.float32(-np.inf) if self.opts["bool_mask"] else MASK_NEG
+        pad = np.where(am == 1, np.float32(0), pad_neg).astype(np.float32)[None, None, :]  # [1, 1, L]
         scale = 1.0 / np.sqrt(np.float32(hd))
         for l in range(self.layers):
             p = f"encoder.layers.{l}"
@@ -163,8 +266,11 @@ class Oracle:
             v = qkv[:, 2 * d:].reshape(L, H, hd).transpose(1, 0, 2)
             cos, sin = self.tables[self.local[l]]
             q, k = rope(q, cos, sin), rope(k, cos, sin)
-            mask = pad + win[None] if self.local[l] else pad
-            att = sdpa(q, k, np.ascontiguousarray(v), scale, mask).transpose(1, 0, 2).reshape(L, d)
+            if self.local[l]:
+                att = local_attention(q, k, np.ascontiguousarray(v), am, scale, self.window, self.opts)
+            else:
+                att = sdpa(q, k, np.ascontiguousarray(v), scale, pad)
+            att = att.transpose(1, 0, 2).reshape(L, d)
             h = h + att @ w[f"{p}.attn.Wo.weight"].T
             m = layer_norm(h, w[f"{p}.mlp_norm.weight"], None, self.eps)
             wi = m @ w[f"{p}.mlp.Wi.weight"].T

@@ -5,8 +5,9 @@ TEST INFRASTRUCTURE, under the same rule as oracle.py: only tests/ may import it
 It takes an oracle.Oracle (the parsed config, the checkpoint widened to f32 and the RoPE tables)
 and performs the same steps in the same order as Oracle._encode_row, Oracle._head_row and
 Oracle.forward (runtime/crates/laya-mlx/src/lib.rs:1525-1800): LayerNorm with f32 mean and
-biased variance, exact-erf GELU, the half-split RoPE rotation, softmax attention with the -1e4
-additive pad and window masks, all in float32 on any torch device. On a GPU it runs the
+biased variance, exact-erf GELU, the half-split RoPE rotation, softmax attention with the
+reference's masks (dense, chunked or banded local attention by the oracle's mask options), all
+in float32 on any torch device. On a GPU it runs the
 8192-token state and the rows of the 64-request sweep in seconds, where the numpy oracle needs
 minutes (its attention is a dense [H, L, L] product per row either way).
 
@@ -60,6 +61,48 @@ class TorchOracle:
         p = e / e.sum(dim=-1, keepdim=True)
         return torch.matmul(p, v.contiguous())
 
+    def local_attention(self, q, k, v, am: np.ndarray, scale: float):
+        """oracle.local_attention in torch: dense, chunked or banded by the oracle's mask options."""
+        o = self.o
+        opts, S = o.opts, o.window
+        L = q.shape[1]
+        dense_upto = opts["dense_upto"] if opts["dense_upto"] is not None else 4 * S
+        banded = opts["band"] > 0 and opts["fuserope"] and not opts["bool_mask"] and L >= opts["band"]
+        chunked = banded or (opts["windowed"] and L > dense_upto)
+        real = torch.from_numpy(am == 1).to(self.dev)
+        zero = torch.tensor(0.0, device=self.dev)
+        neg = torch.tensor(float(O.MASK_NEG), device=self.dev)
+        ninf = torch.tensor(float("-inf"), device=self.dev)
+        if not chunked:
+            idx = torch.arange(L, device=self.dev)
+            inwin = (idx[:, None] - idx[None, :]).abs() <= S
+            if opts["bool_mask"]:
+                mask = torch.where((inwin | ~real[:, None]) & real[None, :], zero, ninf)
+            else:
+                mask = torch.where(real, zero, neg)[None, :] + torch.where(inwin, zero, neg)
+            return self.sdpa(q, k, v, scale, mask[None])
+        H, hd = q.shape[0], q.shape[2]
+        nc = -(-L // S)
+        qp = torch.zeros((H, nc * S, hd), device=self.dev)
+        qp[:, :L] = q
+        qp = qp.reshape(H, nc, S, hd)
+        pos = torch.from_numpy(O.window_positions(S, nc)).to(self.dev)
+        idx = pos.clamp(0, L - 1)
+        kg, vg = k[:, idx], v[:, idx]
+        if banded:
+            out = (pos < 0) | (pos >= L)
+            kg[:, out] = 0
+            vg[:, out] = 0
+        key_ok = torch.from_numpy(O.window_key_valid(am, S, nc)).to(self.dev)
+        band = torch.from_numpy(O.band_allows(S)).to(self.dev)
+        if opts["bool_mask"]:
+            padded = torch.from_numpy(O.window_query_padded(am, S, nc)).to(self.dev)
+            mask = torch.where((key_ok[:, None, :] & band[None]) | padded[:, :, None], zero, ninf)
+        else:
+            mask = torch.where(key_ok, zero, neg)[:, None, :] + torch.where(band, zero, neg)[None]
+        att = self.sdpa(qp, kg, vg, scale, mask[None])
+        return att.reshape(H, nc * S, hd)[:, :L]
+
     # ---- encoder (Oracle._encode_row)
     def _encode_row(self, ids: np.ndarray, am: np.ndarray) -> torch.Tensor:
         o, w = self.o, self.w
@@ -69,11 +112,9 @@ class TorchOracle:
         amt = torch.from_numpy(am.astype(np.int64)).to(self.dev)
         h = self.layer_norm(w["encoder.embeddings.tok_embeddings.weight"][idt], w["encoder.embeddings.norm.weight"],
                             None, o.eps)
-        neg = torch.tensor(float(O.MASK_NEG), device=self.dev)
+        neg = torch.tensor(float("-inf") if o.opts["bool_mask"] else float(O.MASK_NEG), device=self.dev)
         zero = torch.tensor(0.0, device=self.dev)
         pad = torch.where(amt == 1, zero, neg)[None, None, :]
-        idx = torch.arange(L, device=self.dev)
-        win = torch.where((idx[:, None] - idx[None, :]).abs() > o.window, neg, zero)
         scale = float(1.0 / np.sqrt(np.float32(hd)))
         for l in range(o.layers):
             p = f"encoder.layers.{l}"
@@ -84,8 +125,8 @@ class TorchOracle:
             v = qkv[:, 2 * d:].reshape(L, H, hd).transpose(0, 1)
             cos, sin = self.tables[o.local[l]]
             q, k = self.rope(q, cos, sin), self.rope(k, cos, sin)
-            mask = pad + win[None] if o.local[l] else pad
-            att = self.sdpa(q, k, v, scale, mask).transpose(0, 1).reshape(L, d)
+            att = self.local_attention(q, k, v, am, scale) if o.local[l] else self.sdpa(q, k, v, scale, pad)
+            att = att.transpose(0, 1).reshape(L, d)
             h = h + att @ w[f"{p}.attn.Wo.weight"].T
             m = self.layer_norm(h, w[f"{p}.mlp_norm.weight"], None, o.eps)
             wi = m @ w[f"{p}.mlp.Wi.weight"].T

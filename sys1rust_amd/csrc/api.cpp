@@ -153,8 +153,12 @@ int s1_encoder_hidden(s1_model* h, uint32_t n, uint32_t len, uint32_t kmax, cons
   return guard([&] {
     if (!h || !h->m) s1::fail(s1::kBackend, "s1_encoder_hidden: model is NULL");
     if (n && !hidden) s1::fail(s1::kBatch, "s1_encoder_hidden: hidden_out is NULL");
-    s1::Plan p = h->m->plan(n, len, kmax, ids, mask, seq_lens, marker_pos, marker_count, qtype);
-    h->m->encoder_hidden(p, mask, hidden);
+    (void)kmax;
+    (void)marker_pos;
+    (void)marker_count;
+    (void)qtype;
+    s1::Plan p = h->m->plan_padded(n, len, ids, mask, seq_lens);
+    h->m->encoder_hidden(p, hidden);
   });
 }
 

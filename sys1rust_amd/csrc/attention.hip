@@ -701,16 +701,90 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
 }
 
+// Attention of the padded layout's padding queries that the local-attention tiles do not take:
+// those whose softmax the reference's masks leave over a key set other than the real keys of
+// the window. Each entry names the set, as the host works it out from the masks
+// (lib.rs:1241-1310): {query, a0, a1, b0, b1, lo, hi, zeros} = keys [a0, a1) and [b0, b1) (packed
+// indices), key a0 counted 1 + lo times, the last key of the last non-empty range 1 + hi times
+// (gathered slots clamped to one key), and `zeros` slots of zero key and value (score 0, value
+// 0). One wave per (entry, head), 64 keys a step: lane j scores key j of the step in f32, lane d
+// accumulates output dim d.
+template <class E>
+__global__ __launch_bounds__(64) void attn_fallback_kernel(FallbackArgs a) {
+  __shared__ float sp[64];
+  const int fi = blockIdx.x / a.heads, head = blockIdx.x % a.heads;
+  const int4 f0 = reinterpret_cast<const int4*>(a.far)[2 * fi];      // query, a0, a1, b0
+  const int4 f1 = reinterpret_cast<const int4*>(a.far)[2 * fi + 1];  // b1, lo, hi, zeros
+  const int lane = threadIdx.x;
+  const uint16_t* __restrict__ Qh = a.q + size_t(head) * a.T * 64;
+  const uint16_t* __restrict__ Kh = a.k + size_t(head) * a.T * 64;
+  const uint16_t* __restrict__ Vt = a.v + size_t(head) * 64 * a.ldv;
+  float qv[64];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) unpack8<E>(*reinterpret_cast<const uint4*>(Qh + size_t(f0.x) * 64 + c * 8), qv + c * 8);
+  const float sl2 = a.scale * 1.4426950408889634f;
+  // Repeated keys: the weight of n copies is exp2(s + log2 n).
+  const int klo = f0.y, khi = (f1.x > f0.w ? f1.x : f0.z) - 1;
+  const float llo = log2f(float(1 + f1.y)), lhi = log2f(float(1 + f1.z));
+  float m = NEG_INF, l = 0.0f, o = 0.0f;
+  auto keys = [&](int j0, int j1) {
+    for (int b = j0; b < j1; b += 64) {
+      const int j = b + lane;
+      float s = NEG_INF;
+      if (j < j1) {
+        float kv[8], dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          unpack8<E>(*reinterpret_cast<const uint4*>(Kh + size_t(j) * 64 + c * 8), kv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dot = fmaf(qv[c * 8 + e], kv[e], dot);
+        }
+        s = dot * sl2 + (j == klo ? llo : 0.0f) + (j == khi ? lhi : 0.0f);
+      }
+      const float mn = fmaxf(m, wave_max(s));
+      const float p = j < j1 ? __builtin_amdgcn_exp2f(s - mn) : 0.0f;
+      const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+      l = l * alpha + wave_sum(p);
+      o *= alpha;
+      m = mn;
+      sp[lane] = p;
+      __syncthreads();
+      const uint16_t* vr = Vt + size_t(lane) * a.ldv + b;  // dim `lane`, keys b ..
+      const int cnt = min(64, j1 - b);
+      for (int t = 0; t < cnt; ++t) o = fmaf(sp[t], E::f32(vr[t]), o);
+      __syncthreads();
+    }
+  };
+  keys(f0.y, f0.z);
+  keys(f0.w, f1.x);
+  if (f1.w > 0) {  // zero slots: score 0, value 0, weight `zeros`
+    const float sz = log2f(float(f1.w));
+    const float mn = fmaxf(m, sz);
+    const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+    l = l * alpha + __builtin_amdgcn_exp2f(sz - mn);
+    o *= alpha;
+  }
+  a.out[size_t(f0.x) * a.ldo + head * 64 + lane] = E::bits(o / l);
+}
+
 }  // namespace
+
+// Query count of row r: up to q_end[r] when given, else the whole row.
+static int row_queries(const int* row_start, const int* q_end, int r) {
+  return (q_end ? q_end[r] : row_start[r + 1]) - row_start[r];
+}
 
 // Local layers: 128-query tiles (attn_local_kernel) while they give at least one workgroup per
 // CU; a shorter batch takes 32-query tiles whose keys are the tile's window range, split over 4
 // waves (attn_ksplit_kernel<LOCAL>). Windows wider than attn_local_kernel stages keep 128.
-int attn_local_tile(const int* row_start, int n, int heads, int window) {
+static int local_tile(const int* row_start, const int* q_end, int n, int heads, int window) {
   if (window > LMAXW) return LQ;
   long long c = 0;
-  for (int r = 0; r < n; ++r) c += (row_start[r + 1] - row_start[r] + LQ - 1) / LQ;
+  for (int r = 0; r < n; ++r) c += (row_queries(row_start, q_end, r) + LQ - 1) / LQ;
   return c * heads >= 256 ? LQ : 32;
+}
+int attn_local_tile(const int* row_start, int n, int heads, int window) {
+  return local_tile(row_start, nullptr, n, heads, window);
 }
 
 int attn_row_step(int len, int qb) {
@@ -722,29 +796,31 @@ int attn_row_step(int len, int qb) {
 // 256-query tiles (8 waves, every K/V chunk shared by 256 queries) while they give at least one
 // workgroup per CU; then 128 (4 waves) while they give 128 workgroups; a shorter batch takes
 // 32-query tiles whose keys are split over 4 waves (attn_ksplit_kernel).
-int attn_global_tile(const int* row_start, int n, int heads) {
+static int global_tile(const int* row_start, const int* q_end, int n, int heads) {
   auto count = [&](int qb) {
     long long c = 0;
-    for (int r = 0; r < n; ++r) c += (row_start[r + 1] - row_start[r] + qb - 1) / qb;
+    for (int r = 0; r < n; ++r) c += (row_queries(row_start, q_end, r) + qb - 1) / qb;
     return c * heads;
   };
   if (count(256) >= 256) return 256;
   if (count(128) >= 128) return 128;
   return 32;  // attn_ksplit_kernel
 }
+int attn_global_tile(const int* row_start, int n, int heads) { return global_tile(row_start, nullptr, n, heads); }
 
-int attn_plan_tiles(const int* row_start, int n, int heads, int window, std::vector<int>& out) {
-  const int qb = window >= 0 ? attn_local_tile(row_start, n, heads, window) : attn_global_tile(row_start, n, heads);
+int attn_plan_tiles(const int* row_start, int n, int heads, int window, std::vector<int>& out, const int* q_end,
+                    const int* k_end) {
+  const int qb = window >= 0 ? local_tile(row_start, q_end, n, heads, window) : global_tile(row_start, q_end, n, heads);
   for (int r = 0; r < n; ++r) {
-    const int rs = row_start[r], re = row_start[r + 1];
-    const int step = attn_row_step(re - rs, qb);
-    for (int q0 = rs; q0 < re; q0 += step) {
-      const int q1 = std::min(q0 + step, re);
+    const int rs = row_start[r], qe = q_end ? q_end[r] : row_start[r + 1], ke = k_end ? k_end[r] : row_start[r + 1];
+    const int step = attn_row_step(qe - rs, qb);
+    for (int q0 = rs; q0 < qe; q0 += step) {
+      const int q1 = std::min(q0 + step, qe);
       const bool win = window >= 0 && qb == 32;
       out.push_back(q0);
       out.push_back(q1);
       out.push_back(win ? std::max(rs, q0 - window) : rs);
-      out.push_back(win ? std::min(re, q1 + window) : re);
+      out.push_back(win ? std::min(ke, q1 + window) : ke);
     }
   }
   return qb;
@@ -773,6 +849,13 @@ void attn_launch(const AttnArgs& a, hipStream_t st) {
   if (a.ntiles <= 0) return;
   if (a.elem == ELEM_F16) attn_launch_t<F16>(a, st);
   else attn_launch_t<Bf16>(a, st);
+}
+
+void attn_fallback_launch(const FallbackArgs& a, hipStream_t st) {
+  if (a.nfar <= 0) return;
+  const dim3 grid(unsigned(a.nfar) * unsigned(a.heads));
+  if (a.elem == ELEM_F16) hipLaunchKernelGGL(attn_fallback_kernel<F16>, grid, dim3(64), 0, st, a);
+  else hipLaunchKernelGGL(attn_fallback_kernel<Bf16>, grid, dim3(64), 0, st, a);
 }
 
 }  // namespace s1

@@ -104,8 +104,28 @@ int attn_global_tile(const int* row_start, int n, int heads);
 int attn_local_tile(const int* row_start, int n, int heads, int window);
 // Appends the work tiles {q0, q1, k0, k1} of the rows (window < 0: a global layer) to out and
 // returns the queries per tile, the AttnArgs::tile_q to launch them with. Keys [k0, k1) are the
-// row's, or for 32-query local tiles the tile's window range within the row.
-int attn_plan_tiles(const int* row_start, int n, int heads, int window, std::vector<int>& out);
+// row's, or for 32-query local tiles the tile's window range within the row. With q_end / k_end
+// (per row), row r's queries stop at q_end[r] and its keys at k_end[r] instead of at the row's
+// end (the padded layout: every position a query, only the real tokens keys).
+int attn_plan_tiles(const int* row_start, int n, int heads, int window, std::vector<int>& out,
+                    const int* q_end = nullptr, const int* k_end = nullptr);
+
+// Attention of single queries over a key set given per query: the padded layout's padding
+// queries on local layers whose keys under the reference's masks are not the real keys of their
+// window. far: nfar entries of 8 int32 (device, 16-byte aligned) {query, a0, a1, b0, b1, lo, hi,
+// zeros}: keys [a0, a1) and [b0, b1), key a0 counted 1 + lo times, the last key of the last
+// non-empty range 1 + hi times, plus `zeros` slots of zero key and value. Every entry has a key.
+struct FallbackArgs {
+  const uint16_t* q = nullptr;
+  const uint16_t* k = nullptr;
+  const uint16_t* v = nullptr;  // transposed, [H, 64, ldv]
+  uint16_t* out = nullptr;      // [T, ldo]
+  const int* far = nullptr;
+  int nfar = 0, heads = 0, T = 0, ldv = 0, ldo = 0;
+  float scale = 0.125f;
+  int elem = ELEM_BF16;
+};
+void attn_fallback_launch(const FallbackArgs& a, hipStream_t st);
 // The query step that cuts a row of len tokens into tiles of at most qb queries: as many tiles
 // as qb needs, of even sizes rounded up to whole waves (570 tokens at 256: 192, 192, 186), so a
 // row's last tile is not a nearly idle workgroup beside full ones.

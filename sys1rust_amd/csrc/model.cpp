@@ -84,8 +84,8 @@ Settings Settings::parse(const std::string& spec) {
     // Knobs' keys (lib.rs:196-256), with its value checks.
     if (key == "geglu") one_of({"shapeless", "compiled", "plain"});
     else if (key == "addmm") flag();
-    else if (key == "mask") one_of({"bool", "additive"});
-    else if (key == "windowed") flag();
+    else if (key == "mask") s.bool_mask = one_of({"bool", "additive"}) == "bool";
+    else if (key == "windowed") s.windowed = flag();
     else if (key == "clear") s.clear = flag();
     else if (key == "trace") s.trace = flag();
     else if (key == "layers") s.layers = flag();
@@ -101,11 +101,11 @@ Settings Settings::parse(const std::string& spec) {
     } else if (key == "warm") s.warm = list();
     else if (key == "cache") number(value());
     else if (key == "wired") number(value());
-    else if (key == "dense_upto") number(value());
+    else if (key == "dense_upto") s.dense_upto = long(number(value()));
     else if (key == "headprune") s.headprune = flag();
     else if (key == "unpad") s.unpad = flag();
     else if (key == "fuserope") s.fuserope = flag();
-    else if (key == "band") number(value());
+    else if (key == "band") s.band = number(value());
     else if (key == "nax") one_of({"0", "all"});
     else if (key == "directload") flag();
     else if (key == "sharehead") flag();
@@ -567,6 +567,101 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
   return p;
 }
 
+Plan Model::plan_padded(uint32_t n, uint32_t len, const uint32_t* ids, const uint32_t* mask,
+                        const uint64_t* seq_lens) const {
+  Plan p;
+  p.n = int(n);
+  p.len = int(len);
+  p.padded = true;
+  if (n == 0) return p;
+  if (!ids) fail(kBatch, "batch: a required array is NULL");
+  const std::vector<uint64_t> no_markers(n, 0);
+  (void)pack_batch(n, len, 0, mask, seq_lens, nullptr, no_markers.data(), cfg.max_pos);  // the batch checks
+  if (len > uint32_t(cfg.max_pos))
+    fail(kBatch, "batch: len " + std::to_string(len) + " is past max_position_embeddings " +
+                     std::to_string(cfg.max_pos) + " (the padded layout gives every position a RoPE angle)");
+  const int64_t T = int64_t(n) * len;
+  if (T > (int64_t(1) << 30)) fail(kBatch, "batch: too many positions");
+  p.T = int(T);
+  p.row_start.resize(n + 1);
+  for (uint32_t r = 0; r <= n; ++r) p.row_start[r] = int(r * len);
+  std::vector<int>& m = p.meta;
+  m.reserve(size_t(3 * T) + 64);
+  p.off_ids = m.size();
+  for (int64_t t = 0; t < T; ++t) {
+    if (ids[t] >= uint32_t(cfg.vocab))
+      fail(kBatch, "batch: token id " + std::to_string(ids[t]) + " in row " + std::to_string(t / len) +
+                       " is past the vocabulary");
+    m.push_back(int(ids[t]));
+  }
+  p.off_pos = m.size();
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t q = 0; q < len; ++q) m.push_back(int(q));
+  p.off_seg = m.size();
+  m.insert(m.end(), size_t(T), 0);
+  auto pad4 = [&]() {
+    while (m.size() % 4) m.push_back(0);
+  };
+  pad4();
+  // Keys of a padding query at position q of a row with L real tokens (positions relative to the
+  // row). Global layers: the real keys [0, L) under either mask form (lib.rs:1227-1235). Local
+  // layers, by the path the reference takes for the batch's len (lib.rs:1241-1270):
+  //  additive masks (the key-padding mask plus the window mask, -1e4 each): a query with a real
+  //   key within the window (q < L + window) sees those keys alone, as a real token does (the
+  //   local tiles take it). A farther one gets -1e4 on every key it can reach and sees them all:
+  //   dense: the real keys [0, L) and the window [q - W, q + W] within the row;
+  //   chunked (S = W; chunk c = q / S gathers positions (c - 1) S .. (c + 2) S - 1, clamped to
+  //   the row, lib.rs:804-814): the real keys among them and the window, the window's positions
+  //   past the row each one more copy of key len - 1;
+  //   banded: as chunked, with zero key and value at the positions past the row (the banded
+  //   layout is zero outside the sequence, split_rope.rs:18-21);
+  //  boolean masks: every padding query sees every real key (dense, lib.rs:1259-1264) or every
+  //   gathered slot, clamped positions included (chunked, lib.rs:1279-1291).
+  const int W = cfg.window(), S = W;
+  const long dense_upto = set.dense_upto >= 0 ? set.dense_upto : 4L * W;
+  const bool banded = set.band > 0 && set.fuserope && !set.bool_mask && len >= set.band;
+  const bool chunked = banded || (set.windowed && long(len) > dense_upto);
+  std::vector<int> kend(n), lqend(n), far;
+  for (uint32_t r = 0; r < n; ++r) {
+    const int rs = p.row_start[r], L = int(seq_lens[r]), ln = int(len);
+    kend[r] = rs + L;
+    lqend[r] = rs + (set.bool_mask ? L : std::min(ln, L + W));
+    for (int q = lqend[r] - rs; q < ln; ++q) {
+      const int c = q / S, g0 = (c - 1) * S, g1 = (c + 2) * S;  // the chunk's gathered positions
+      int e[8] = {rs + q, rs, rs, rs, rs, 0, 0, 0};
+      if (set.bool_mask && !chunked) {
+        e[2] = rs + L;
+      } else if (set.bool_mask) {
+        e[1] = rs + std::max(0, g0);
+        e[2] = rs + std::min(ln, g1);
+        e[5] = std::max(0, -g0);
+        e[6] = std::max(0, g1 - ln);
+      } else {
+        const int a0 = chunked ? std::max(0, g0) : 0;
+        e[1] = rs + std::min(a0, L);
+        e[2] = rs + L;
+        e[3] = rs + q - W;
+        e[4] = rs + std::min(ln, q + W + 1);
+        const int past = std::max(0, q + W + 1 - ln);  // window positions past the row
+        if (banded) e[7] = past;
+        else if (chunked) e[6] = past;
+      }
+      far.insert(far.end(), e, e + 8);
+    }
+  }
+  p.off_tiles = m.size();
+  p.gq = attn_plan_tiles(p.row_start.data(), int(n), cfg.heads, -1, m, nullptr, kend.data());
+  p.ntiles = int(m.size() - p.off_tiles) / 4;
+  p.off_ltiles = m.size();
+  p.lq = attn_plan_tiles(p.row_start.data(), int(n), cfg.heads, W, m, lqend.data(), kend.data());
+  p.nltiles = int(m.size() - p.off_ltiles) / 4;
+  p.off_far = m.size();
+  m.insert(m.end(), far.begin(), far.end());
+  p.nfar = int(far.size() / 8);
+  p.off_scorer = p.off_pooled = m.size();
+  return p;
+}
+
 void Model::upload(const Plan& p) {
   const size_t bytes = p.meta.size() * 4;
   if (bytes > hmeta_cap) {
@@ -821,6 +916,23 @@ int Model::run_encoder(const Plan& p, const Acts& a, bool fold_last) {
       at.tile_q = L.local ? p.lq : p.gq;
       attn_launch(at, stream);
     });
+    if (L.local && p.nfar > 0)
+      op("attn_far_pad", [&] {
+        FallbackArgs fa;
+        fa.elem = elem;
+        fa.q = a.q;
+        fa.k = a.k;
+        fa.v = a.v;
+        fa.out = a.att;
+        fa.far = dmeta + p.off_far;
+        fa.nfar = p.nfar;
+        fa.heads = H;
+        fa.T = T;
+        fa.ldv = vt_ld(T);
+        fa.ldo = d;
+        fa.scale = 1.0f / std::sqrt(float(cfg.head_dim()));
+        attn_fallback_launch(fa, stream);
+      });
     x_ready = false;
     // h = h + att . Wo^T (lib.rs:1666), x = mlp_norm(h) (lib.rs:1669)
     // Wo and Wo2 plan their split as finished by the LayerNorm after them (structurally, so the
@@ -878,7 +990,8 @@ void Model::run(const Plan& p, int kind, F&& enqueue) {
   std::vector<int64_t> key = {kind, p.T, p.n, p.kmax, p.gq, p.lq, p.ntiles, p.nltiles, p.nptiles, p.P, p.R, int64_t(p.off_ltiles),
                               int64_t(p.off_ids), int64_t(p.off_pos), int64_t(p.off_seg), int64_t(p.off_tiles),
                               int64_t(p.off_ptiles), int64_t(p.off_picked), int64_t(p.off_scorer),
-                              int64_t(p.off_pooled), int64_t(reinterpret_cast<intptr_t>(amem)),
+                              int64_t(p.off_pooled), int64_t(p.off_far), p.nfar, int64_t(p.padded),
+                              int64_t(reinterpret_cast<intptr_t>(amem)),
                               int64_t(reinterpret_cast<intptr_t>(dmeta))};
   ++graph_clock;
   for (auto& g : graphs)
@@ -1143,8 +1256,9 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
   if (set.clear) release();
 }
 
-void Model::encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden) {
+void Model::encoder_hidden(const Plan& p, float* hidden) {
   if (p.n == 0) return;
+  if (!p.padded) fail(kBackend, "encoder_hidden: the plan is not the padded layout");
   hip_check(hipSetDevice(device), "hipSetDevice");
   upload(p);
   Acts a = arena(p);
@@ -1156,18 +1270,11 @@ void Model::encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden) {
                        nullptr, stream, elem);
     });
   });
-  std::vector<float> packed(size_t(T) * d);
-  hip_check(hipMemcpyAsync(packed.data(), a.enc, packed.size() * 4, hipMemcpyDeviceToHost, stream), "download hidden");
+  // The padded layout's rows are the [n, len] positions in order: [T, d] is [n, len, d].
+  hip_check(hipMemcpyAsync(hidden, a.enc, size_t(T) * d * 4, hipMemcpyDeviceToHost, stream), "download hidden");
   hip_check(hipStreamSynchronize(stream), "encoder_hidden");
   if (set.ops) collect_stats();
   if (set.layers) layer_report();
-  // Expand [T, d] -> [n, len, d]; padding positions are not computed and read 0.
-  std::memset(hidden, 0, size_t(p.n) * p.len * d * 4);
-  for (int r = 0; r < p.n; ++r) {
-    const int rs = p.row_start[r], sl = p.row_start[r + 1] - rs;
-    std::memcpy(hidden + size_t(r) * p.len * d, packed.data() + size_t(rs) * d, size_t(sl) * d * 4);
-  }
-  (void)mask;
   if (set.clear) release();
 }
 

@@ -29,12 +29,19 @@ struct Settings {
   size_t pad = 1;          // padded_len multiple
   std::vector<size_t> buckets;
   std::vector<size_t> warm;  // row counts to run one forward for at every bucket length at load
+  // The reference's local-attention mask choices (lib.rs:1241-1270). At real tokens every choice
+  // gives the same attention (masks are exact exclusion here, the same values as either MLX
+  // form), so the forward ignores them; the padded layout of encoder_hidden follows them at the
+  // padding positions, whose key sets they decide.
+  bool bool_mask = false;  // mask=bool
+  bool windowed = true;    // chunked local attention above dense_upto
+  long dense_upto = -1;    // -1: 4 * window
+  size_t band = 0;         // banded (zero-filled) chunks from this padded length up; needs fuserope
   // Keys of Knobs whose MLX mechanism has no counterpart here; parsed and checked, no effect:
-  // unpad (this path always runs the packed token layout), band / dense_upto / windowed (local
-  // attention is always the exact windowed kernel), mask (masks are exact exclusion, the same
-  // values as either MLX form), geglu / f16gelu (GeGLU always in f32), addmm (the residual add
-  // is always in the GEMM epilogue), nax / wcopy / directload / sharehead (weight layout and
-  // MLX gemm choice), cache / wired (MLX memory limits), parallel_load (the runtime's).
+  // unpad (this path always runs the packed token layout), geglu / f16gelu (GeGLU always in
+  // f32), addmm (the residual add is always in the GEMM epilogue), nax / wcopy / directload /
+  // sharehead (weight layout and MLX gemm choice), cache / wired (MLX memory limits),
+  // parallel_load (the runtime's).
   bool unpad = false;
   // This backend's own.
   bool fusegeglu = true;   // GeGLU fused into the Wi GEMM epilogue (Wi rows interleaved at load)
@@ -82,7 +89,7 @@ Packed pack_batch(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* mask,
 // A validated batch in packed form, plus every index table the kernels read.
 struct Plan {
   int n = 0, len = 0, kmax = 0;
-  int T = 0;  // real tokens
+  int T = 0;  // rows of the forward: the real tokens (packed layout) or n * len (padded)
   int P = 0;  // picked rows of the pruned head layer (n * (1 + kmax))
   int R = 0;  // scorer rows (n * kmax)
   std::vector<int> row_start;  // [n + 1]
@@ -93,6 +100,13 @@ struct Plan {
   int ntiles = 0, nltiles = 0, nptiles = 0;
   int gq = 256;  // queries per global-attention tile
   int lq = 128;  // queries per local-attention tile
+  // The padded layout (encoder_hidden): every one of the n * len positions is a row of the
+  // forward (T = n * len). The local-attention tiles take the real tokens and the padding
+  // queries whose keys are the real keys of their window; the other padding queries of local
+  // layers are listed at off_far with their key sets (attn_fallback_launch's entries).
+  bool padded = false;
+  size_t off_far = 0;
+  int nfar = 0;
 };
 
 struct Model {
@@ -163,8 +177,10 @@ struct Model {
   Plan plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, const uint32_t* mask,
             const uint64_t* seq_lens, const uint32_t* marker_pos, const uint64_t* marker_count,
             const uint32_t* qtype) const;
+  // The encoder over the padded layout (plan_padded), as MlxBackend::encoder_hidden runs it.
+  Plan plan_padded(uint32_t n, uint32_t len, const uint32_t* ids, const uint32_t* mask, const uint64_t* seq_lens) const;
   void forward(const Plan& p, float* logits, float* pooled);
-  void encoder_hidden(const Plan& p, const uint32_t* mask, float* hidden);
+  void encoder_hidden(const Plan& p, float* hidden);
   size_t padded_len(size_t len) const;
 
  private:

@@ -22,10 +22,13 @@ def say(*a):
     print(*a, flush=True)
 
 
-def hidden_rel(gpu_hidden: np.ndarray, ref: np.ndarray, b: Batch) -> float:
+def hidden_rel(gpu_hidden: np.ndarray, ref: np.ndarray, b: Batch, padding: bool = False) -> float:
+    """Worst ||gpu - ref|| / ||ref|| over the real tokens, or over every position with padding
+    (the reference and the checker then have to share the mask settings, which decide the
+    padding positions' attention)."""
     g = gpu_hidden.reshape(b.n, b.len, -1)
-    am = b.attention_mask.reshape(b.n, b.len).astype(bool)
-    d = np.linalg.norm(g[am] - ref[am], axis=-1) / np.linalg.norm(ref[am], axis=-1)
+    sel = np.ones((b.n, b.len), bool) if padding else b.attention_mask.reshape(b.n, b.len).astype(bool)
+    d = np.linalg.norm(g[sel] - ref[sel], axis=-1) / np.linalg.norm(ref[sel], axis=-1)
     return float(d.max())
 
 

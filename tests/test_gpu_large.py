@@ -13,6 +13,7 @@ output is finite. The model runs sys1rust's production settings (DEFAULT_TUNING)
 """
 from __future__ import annotations
 
+import copy
 import json
 
 import numpy as np
@@ -30,9 +31,14 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(scope="module")
-def big():
+def big_ckpt():
     say("big: synth checkpoint")
-    st = synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
+    return synth_checkpoint(json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), seed=2024, scorer_width=1024)
+
+
+@pytest.fixture(scope="module")
+def big(big_ckpt):
+    st = big_ckpt
     say("big: create")
     m = HipBackend(st, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT), settings=DEFAULT_TUNING)
     o = O.Oracle(st, MODERNBERT_LARGE, AGENT)
@@ -136,3 +142,35 @@ def test_sweep64_packed_batch_every_row(big):
     sub = b.rows(rows)
     alone = m.forward(sub)
     check_answers(alone.logits, lg_all[rows].reshape(-1), sub, "sweep64 rows alone")
+
+
+@pytest.mark.parametrize("settings", ["", "mask=bool", DEFAULT_TUNING])
+def test_encoder_hidden_padding_positions_large(big, big_ckpt, settings):
+    """The ModernBERT-large encoder at a 600-position padded length, where the reference's local
+    layers run chunked (default settings, boolean masks) or banded (DEFAULT_TUNING: band=512):
+    every position of rows with 600, 300 and 20 real tokens (padding far past the window, and
+    padding queries in the first chunk), against the torch checker under the same masks."""
+    m0, o0, t0 = big
+    lens, L = [600, 300, 20], 600
+    rng = np.random.default_rng(17)
+    ids = rng.integers(5, 50000, size=(len(lens), L)).astype(np.uint32)
+    am = np.zeros((len(lens), L), np.uint32)
+    for r, l in enumerate(lens):
+        am[r, :l] = 1
+        ids[r, l:] = 50283
+    b = Batch(len(lens), L, 0, ids.reshape(-1), am.reshape(-1), np.array(lens, np.uint64), np.zeros(0, np.uint32),
+              np.zeros(len(lens), np.uint64), np.zeros(len(lens), np.uint32))
+    o = copy.copy(o0)
+    o.opts = O.mask_options(settings)
+    t = copy.copy(t0)
+    t.o = o
+    m = m0 if settings == DEFAULT_TUNING else HipBackend(big_ckpt, json.dumps(MODERNBERT_LARGE), json.dumps(AGENT),
+                                                         settings=settings)
+    say(f"padding large {settings[:40]!r}: n={b.n} len={b.len}")
+    ref = t.encoder_hidden(b)
+    hid = m.encoder_hidden(b).reshape(b.n, b.len, -1)
+    rel = hidden_rel(hid, ref, b, padding=True)
+    say(f"padding large {settings[:40]!r}: hidden rel at every position {rel:.2e}")
+    assert rel <= HIDDEN_REL_GATE, rel
+    if m is not m0:
+        m.close()

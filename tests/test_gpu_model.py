@@ -63,14 +63,50 @@ def test_small_encoder_matches_oracle_and_golden(small_model, small_ref):
     assert m.active_kernels() == ["fusegeglu", "fuseln"]
     gate_model(m, b, ref, lg_ref, pl_ref, act, "small default")
     hid = m.encoder_hidden(b).reshape(b.n, b.len, -1)
-    # padding positions are not computed
-    am = b.attention_mask.reshape(b.n, b.len).astype(bool)
-    assert np.all(hid[~am] == 0)
+    # every position, padding included, as the oracle computes it under the same (default) masks
+    assert hidden_rel(hid, ref, b, padding=True) <= HIDDEN_REL_GATE
     # against the independent golden values too
     sel = z["hidden_sel"]
     g = hid[sel[:, 0], sel[:, 1]]
     gr = float((np.linalg.norm(g - z["hidden"], axis=-1) / np.linalg.norm(z["hidden"], axis=-1)).max())
     assert gr <= HIDDEN_REL_GATE, gr
+
+
+# The reference's local-attention mask paths (lib.rs:1241-1310) that tell the padding positions
+# apart, on the small model (window 16, dense up to 64 positions by default).
+PADDING_MODES = ["", "dense_upto=0", "band=1,fuserope", "mask=bool", "mask=bool,dense_upto=0", DEFAULT_TUNING,
+                 "windowed=0,dtype=f16"]
+
+
+@pytest.mark.parametrize("settings", PADDING_MODES)
+def test_encoder_hidden_padding_positions(small_model, settings):
+    """encoder_hidden at every position, padding included, under each mask path the reference
+    takes (dense, chunked, banded, boolean dense and chunked): the padding queries' key sets
+    differ per path, and the oracle runs the same path. Rows with padding within the window of
+    their last real token and beyond it, a far padding query in the first chunk (5 real tokens),
+    a 1-token row and a full row."""
+    cfg, agent, st, b0, z = small_model
+    o = O.Oracle(st, cfg, agent, settings=settings)
+    lens, L = [5, 40, 1], 40
+    rng = np.random.default_rng(11)
+    ids = rng.integers(5, 1000, size=(len(lens), L)).astype(np.uint32)
+    am = np.zeros((len(lens), L), np.uint32)
+    for r, l in enumerate(lens):
+        am[r, :l] = 1
+        ids[r, l:] = 1002
+    b1 = Batch(len(lens), L, 0, ids.reshape(-1), am.reshape(-1), np.array(lens, np.uint64), np.zeros(0, np.uint32),
+               np.zeros(len(lens), np.uint64), np.zeros(len(lens), np.uint32))
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=settings)
+    for tag, b in (("golden batch", b0), ("short rows", b1)):
+        say(f"padding {settings!r}: {tag} n={b.n} len={b.len}")
+        ref = o.encoder_hidden(b)
+        hid = m.encoder_hidden(b).reshape(b.n, b.len, -1)
+        rel = hidden_rel(hid, ref, b, padding=True)
+        say(f"padding {settings!r}: {tag}: hidden rel at every position {rel:.2e}")
+        assert rel <= HIDDEN_REL_GATE, (settings, tag, rel)
+        # the same call again (graph replay of the padded layout)
+        assert np.array_equal(hid, m.encoder_hidden(b).reshape(b.n, b.len, -1))
+    m.close()
 
 
 @pytest.mark.parametrize("head_layers", [0, 1])
@@ -173,7 +209,9 @@ def test_batch_without_markers(small_model):
 ])
 def test_settings_variants_match_oracle(small_model, small_ref, settings):
     """Each settings variant on its own against the oracle. The MLX-only keys of the last variant
-    are accepted without effect: the same kernels run, so its bits equal DEFAULT_TUNING's."""
+    are accepted without effect on the forward: the same kernels run, so its bits equal
+    DEFAULT_TUNING's (mask / windowed / band choose only the padding positions' keys in
+    encoder_hidden)."""
     cfg, agent, st, b, z = small_model
     o, ref, lg_ref, pl_ref, act = small_ref
     say(f"variant {settings}")
@@ -185,7 +223,9 @@ def test_settings_variants_match_oracle(small_model, small_ref, settings):
         base = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=DEFAULT_TUNING)
         o1 = base.forward(b)
         assert np.array_equal(o1.logits, out.logits) and np.array_equal(o1.pooled, out.pooled)
-        assert np.array_equal(base.encoder_hidden(b), m.encoder_hidden(b))
+        # at the real tokens: mask=bool gives the padding positions other keys, as in the reference
+        real = np.repeat(b.attention_mask.astype(bool), cfg["hidden_size"])
+        assert np.array_equal(base.encoder_hidden(b)[real], m.encoder_hidden(b)[real])
         base.close()
     m.close()
 

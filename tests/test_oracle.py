@@ -250,3 +250,137 @@ def test_local_window_is_exactly_local(small):
         out = o._encode_row(ids2, am)
         diff = float(np.abs(out[2] - base[2]).max())
         assert (diff > 0) == changed, (dist, diff)
+
+
+# ---- the local-attention paths the reference picks per batch length (lib.rs:1241-1310)
+MODES = {
+    "dense": "windowed=0",
+    "chunked": "dense_upto=0",
+    "banded": "band=1,fuserope",
+    "bool_dense": "mask=bool,windowed=0",
+    "bool_chunked": "mask=bool,dense_upto=0",
+}
+
+
+def test_chunk_tables_known_answers():
+    """The reference's own fixture (lib.rs:2175-2180): S = 2, len = 7, row 0 all real, row 1 three
+    real tokens. Tables written out by hand from the position rule (slot j of chunk c holds
+    position (c - 1) S + j); row 1's fourth chunk holds no valid key (lib.rs:2246-2247)."""
+    T, F = True, False
+    rows = [np.ones(7, np.uint32), np.array([1, 1, 1, 0, 0, 0, 0], np.uint32)]
+    want_keys = [
+        [[F, F, T, T, T, T], [T, T, T, T, T, T], [T, T, T, T, T, F], [T, T, T, F, F, F]],
+        [[F, F, T, T, T, F], [T, T, T, F, F, F], [T, F, F, F, F, F], [F, F, F, F, F, F]],
+    ]
+    want_padded = [
+        [[F, F], [F, F], [F, F], [F, T]],
+        [[F, F], [F, T], [T, T], [T, T]],
+    ]
+    for am, wk, wp in zip(rows, want_keys, want_padded):
+        assert O.window_key_valid(am, 2, 4).tolist() == wk
+        assert O.window_query_padded(am, 2, 4).tolist() == wp
+    # lib.rs:2202-2210: band[i, j] iff i + 2S >= j >= i
+    assert O.band_allows(2).tolist() == [[T, T, T, T, T, F], [F, T, T, T, T, T]]
+
+
+def _brute_local(q, k, v, am, scale, S, mode):
+    """One query at a time, one key slot at a time, from the rules as the reference states them:
+    dense masks over the row's keys, or the chunk's 3S gathered slots (position (c - 1) S + j,
+    clamped to the row; zero outside it when banded), -1e4 per failed test (additive) or
+    exclusion (boolean, padding queries seeing every valid key / every slot)."""
+    H, L, hd = q.shape
+    out = np.zeros_like(q, dtype=np.float64)
+    chunked = mode in ("chunked", "banded", "bool_chunked")
+    boolean = mode.startswith("bool")
+    for h in range(H):
+        for t in range(L):
+            pad_q = am[t] != 1
+            scores, vals = [], []
+            slots = range(3 * S) if chunked else range(L)
+            for j in slots:
+                p = (t // S - 1) * S + j if chunked else j
+                inside = 0 <= p < L
+                pc = min(max(p, 0), L - 1)
+                valid = inside and am[pc] == 1
+                inband = abs(t - p) <= S
+                kk, vv = k[h, pc].astype(np.float64), v[h, pc].astype(np.float64)
+                if mode == "banded" and not inside:
+                    kk, vv = np.zeros(hd), np.zeros(hd)
+                s = float(q[h, t].astype(np.float64) @ kk) * scale
+                if boolean:
+                    if not ((valid and inband) or (pad_q and (chunked or valid))):
+                        continue
+                else:  # the masks are added to the f32 score in f32, as the oracle and MLX's f32 path do
+                    s = float(np.float32(s) + np.float32((0.0 if valid else -1e4) + (0.0 if inband else -1e4)))
+                scores.append(s)
+                vals.append(vv)
+            sc = np.array(scores)
+            w = np.exp(sc - sc.max())
+            out[h, t] = (w[:, None] * np.array(vals)).sum(0) / w.sum()
+    return out
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_local_attention_paths_brute_force(mode):
+    """oracle.local_attention on every path against the slot-by-slot restatement, at every query
+    of rows with padding up to and beyond the window, and a length that is not a multiple of S."""
+    rng = np.random.default_rng(3)
+    H, hd, S = 2, 8, 4
+    opts = O.mask_options(MODES[mode])
+    for L, real in [(23, 9), (16, 16), (13, 1), (8, 5)]:
+        q, k, v = (rng.standard_normal((H, L, hd)).astype(np.float32) for _ in range(3))
+        am = (np.arange(L) < real).astype(np.uint32)
+        got = O.local_attention(q, k, v, am, 0.35, S, opts)
+        want = _brute_local(q, k, v, am, 0.35, S, mode)
+        # 1e-3: a score near -1e4 holds 2^-10 in f32, so an f32 rounding flip there moves a weight by 0.1 %
+        np.testing.assert_allclose(got, want, rtol=2e-4, atol=1e-3, err_msg=f"{mode} L={L} real={real}")
+        real_rows = np.arange(L) < real
+        np.testing.assert_allclose(got[:, real_rows], want[:, real_rows], rtol=2e-4, atol=2e-5)
+
+
+def test_local_attention_paths_agree_at_real_tokens():
+    """Every path gives a real token the same attention (the real keys of its window): they differ
+    at padding queries only, and there each path's padding outputs differ from the dense ones."""
+    rng = np.random.default_rng(5)
+    H, hd, S, L, real = 2, 8, 4, 29, 11
+    q, k, v = (rng.standard_normal((H, L, hd)).astype(np.float32) for _ in range(3))
+    am = (np.arange(L) < real).astype(np.uint32)
+    outs = {m: O.local_attention(q, k, v, am, 0.35, S, O.mask_options(s)) for m, s in MODES.items()}
+    for m, o in outs.items():
+        np.testing.assert_allclose(o[:, :real], outs["dense"][:, :real], rtol=1e-5, atol=1e-6, err_msg=m)
+        if m != "dense":
+            assert float(np.abs(o[:, real + S + 1:] - outs["dense"][:, real + S + 1:]).max()) > 1e-3, m
+
+
+def test_mask_path_follows_len():
+    """Chunked local attention from dense_upto + 1 (default 4 * window) when windowed, banded from
+    `band` when fuserope is on, dense otherwise: the oracle's choice, seen through the padding
+    outputs."""
+    rng = np.random.default_rng(9)
+    H, hd, S = 1, 8, 2
+    for L, settings, path in [(8, "", "dense"), (9, "", "chunked"), (9, "windowed=0", "dense"),
+                              (9, "dense_upto=9", "dense"), (6, "band=6,fuserope", "banded"),
+                              (6, "band=6", "dense"), (5, "band=6,fuserope", "dense")]:
+        q, k, v = (rng.standard_normal((H, L, hd)).astype(np.float32) for _ in range(3))
+        am = (np.arange(L) < 2).astype(np.uint32)
+        got = O.local_attention(q, k, v, am, 0.35, S, O.mask_options(settings))
+        np.testing.assert_allclose(got, _brute_local(q, k, v, am, 0.35, S, path), rtol=2e-4, atol=1e-3,
+                                   err_msg=f"L={L} {settings}")
+
+
+def test_mask_paths_change_the_padding_hidden_states(small):
+    """On the golden batch (window 16; a row with padding past the window of its last real token),
+    the mask paths give the same hidden states at the real tokens and, at the padding positions,
+    states apart by more than twice the GPU parity gate (2e-2 relative): that gate tells the
+    paths apart."""
+    z, cfg, agent, b, st = small
+    am = b.attention_mask.reshape(b.n, b.len).astype(bool)
+    encs = {m: O.Oracle(st, cfg, agent, settings=s).encoder_hidden(b) for m, s in MODES.items()}
+    base = encs["dense"]
+    for m, e in encs.items():
+        np.testing.assert_allclose(e[am], base[am], rtol=1e-5, atol=1e-5, err_msg=m)
+        for m2, e2 in encs.items():
+            if m2 <= m:
+                continue
+            rel = np.linalg.norm(e[~am] - e2[~am], axis=-1) / np.linalg.norm(e2[~am], axis=-1)
+            assert float(rel.max()) > 0.05, (m, m2, float(rel.max()))
