@@ -9,6 +9,7 @@ transformers' ModernBertModel at this shape, and against the oracle on every row
 """
 from __future__ import annotations
 
+import copy
 import json
 from pathlib import Path
 
@@ -20,7 +21,7 @@ from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
 from sys1rust_amd.decode import ActHead
 from sys1rust_amd.workloads import MMBERT_BASE, Batch, workload
 
-from gates import FUSED, HIDDEN_REL_GATE, gate_model, say
+from gates import FUSED, HIDDEN_REL_GATE, gate_model, hidden_rel, say
 
 pytestmark = pytest.mark.gpu
 
@@ -85,3 +86,30 @@ def test_mmbert_base_f16(mmbert):
     lg, pl = o.forward(b, ref)
     gate_model(m16, b, ref, lg, pl, act, "mmbert f16 state512_1q")
     m16.close()
+
+
+@pytest.mark.parametrize("settings", ["", DEFAULT_TUNING + ",dtype=f16"])
+def test_mmbert_encoder_hidden_padding_positions(mmbert, settings):
+    """encoder_hidden at every position at this shape (window 64): a 300-position padded length,
+    chunked local attention under the default settings and dense under DEFAULT_TUNING
+    (dense_upto=1024), rows of 300, 40 and 2 real tokens, against the oracle under the same
+    settings."""
+    _, o0, st, _ = mmbert
+    lens, L = [300, 40, 2], 300
+    rng = np.random.default_rng(23)
+    ids = rng.integers(5, 250000, size=(len(lens), L)).astype(np.uint32)
+    am = np.zeros((len(lens), L), np.uint32)
+    for r, l in enumerate(lens):
+        am[r, :l] = 1
+        ids[r, l:] = MMBERT_BASE["pad_token_id"]
+    b = Batch(len(lens), L, 0, ids.reshape(-1), am.reshape(-1), np.array(lens, np.uint64), np.zeros(0, np.uint32),
+              np.zeros(len(lens), np.uint64), np.zeros(len(lens), np.uint32))
+    o = copy.copy(o0)
+    o.opts = O.mask_options(settings)
+    m = HipBackend(st, json.dumps(MMBERT_BASE), json.dumps(AGENT_ML), settings=settings)
+    say(f"mmbert padding {settings[:30]!r}: n={b.n} len={b.len}")
+    ref = o.encoder_hidden(b)
+    rel = hidden_rel(m.encoder_hidden(b).reshape(b.n, b.len, -1), ref, b, padding=True)
+    say(f"mmbert padding {settings[:30]!r}: hidden rel at every position {rel:.2e}")
+    assert rel <= HIDDEN_REL_GATE, rel
+    m.close()
