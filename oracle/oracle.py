@@ -176,7 +176,7 @@ def local_attention(q, k, v, am, scale: float, window: int, opts: dict) -> np.nd
     takes for this len (lib.rs:1241-1270): dense pad + window masks, chunked (1428-1475: queries
     in chunks of S = window against the 3S gathered keys of chunks c - 1, c, c + 1, clamped to
     the row), or banded (the chunked sdpa on a layout that is zero outside the row,
-    split_rope.rs:18-21). Additive masks add -1e4 per failed test; boolean masks exclude, and
+    split_rope.rs:56-59 and its test mlx_path_band_is_the_chunked_view, 622-657). Additive masks add -1e4 per failed test; boolean masks exclude, and
     padding queries may see every valid key (dense) or every gathered slot (chunked)."""
     L = q.shape[1]
     S = window
