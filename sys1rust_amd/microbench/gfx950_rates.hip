@@ -1,7 +1,8 @@
 // Per-CU rates of the units the GEMMs and attention kernels lean on, measured on one MI355X:
 // the MFMA pipe (v_mfma_f32_32x32x16_bf16), LDS reads (ds_read_b128), global -> LDS direct loads
 // (global_load_lds_dwordx4) and global -> VGPR loads from an L2-resident buffer, and the mix of
-// MFMA and LDS reads that a GEMM wave runs (with and without direct loads beside it). Each line
+// MFMA and LDS reads that a GEMM wave runs (with and without direct loads beside it), and the
+// VALU issue of the softmax's exp2 against FMAs. Each line
 // prints the wall time, the shader clock the kernel ran at (s_memtime against the 100 MHz
 // s_memrealtime) and the rate. Build and run on the GPU host:
 //   hipcc -O3 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops \
@@ -174,6 +175,27 @@ __global__ __launch_bounds__(256) void k_mix(int iters, float* out, Clk* clk, co
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// VALU issue: 8 independent chains per lane of v_exp_f32 (MODE 0), v_fma_f32 (1), or half of
+// each in every wave (2). Whether the transcendental overlaps the FMAs of the same wave shows in
+// mode 2's time against the sum of the halves of modes 0 and 1.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_valu(int iters, float* out, Clk* clk, const uint16_t*) {
+  float x[8];
+  for (int i = 0; i < 8; ++i) x[i] = threadIdx.x * 1e-4f - i * 0.01f;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool ex = MODE == 0 || (MODE == 2 && (i & 1) == 0);
+      x[i] = ex ? __builtin_amdgcn_exp2f(x[i]) : fmaf(x[i], 0.999f, 1e-3f);
+    }
+  }
+  stamp(clk, t0, r0);
+  float s = 0;
+  for (int i = 0; i < 8; ++i) s += x[i];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 template <class K>
 void run(const char* name, K kern, int grid, int iters, double flop_per_wave_iter, double bytes_per_wave_iter,
          const uint16_t* src) {
@@ -223,6 +245,10 @@ int main() {
   run("mfma+lds 96x64 wave, 16 k-tiles/WG", k_mix<3, 2, 0>, 1536, 16, 4 * 6 * mf, 4 * 5 * 1024, src);
   run("mfma+lds 128x128 wave, 1 per CU", k_mix<4, 4, 0>, 256, 2000, 4 * 16 * mf, 4 * 8 * 1024, src);
   run("mfma+lds 32x64 wave, 768 WGs", k_mix<1, 2, 0>, 768, 2000, 4 * 2 * mf, 4 * 3 * 1024, src);
+  // The "TFLOP/s" column of these three is T lane-instructions/s (8 per lane per iteration).
+  run("valu: exp2 only", k_valu<0>, 2048, 10000, 8 * 64, 0, src);
+  run("valu: fma only", k_valu<1>, 2048, 10000, 8 * 64, 0, src);
+  run("valu: half exp2, half fma per wave", k_valu<2>, 2048, 10000, 8 * 64, 0, src);
   CK(hipFree(src));
   return 0;
 }
