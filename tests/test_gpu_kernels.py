@@ -219,13 +219,14 @@ def attention_ref(q, k, v, starts, window, scale):
     return out
 
 
-# window 64 and 16 take the staged local kernel ([2048], 24 rows of 600) or, for the shorter
-# batches, 32-query tiles of the window range with the keys split over 4 waves; 100 takes the
-# chunked one; -1 the global one, whose tiles hold 32 queries with the keys split over 4 waves
-# ([8, 200], [700, 1], [513]), 128 (the other short batches) or 256 (24 rows of 600)
+# window 64 and 16 take the staged local kernel ([2048], 24 rows of 600, and the 28 mixed rows
+# of 1 to 600 tokens, whose tiles include one-token rows and waves past their tile's queries) or,
+# for the shorter batches, 32-query tiles of the window range with the keys split over 4 waves;
+# 100 takes the chunked one; -1 the global one, whose tiles hold 32 queries with the keys split
+# over 4 waves ([8, 200], [700, 1], [513]), 128 (the other short batches) or 256 (24 rows of 600)
 @pytest.mark.parametrize("window", [-1, 64, 16, 100])
 @pytest.mark.parametrize("lens", [[1, 37, 129, 300, 600], [8, 200], [700, 1], [513], [2048], [5, 3, 250, 1, 700, 9],
-                                  [600] * 24])
+                                  [600] * 24, [1, 2, 130, 7, 64, 600, 3] * 4])
 def test_attention_varlen(dev, window, lens):
     say(f"attention window={window} lens={lens}")
     H = 16
