@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
+from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, S1Error, synth_checkpoint
 from sys1rust_amd.decode import ActHead
 from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, Batch, workload
 
@@ -126,6 +126,33 @@ def test_decision_head_depths(small_model, head_layers):
         outs.append(gate_model(m, b, ref, lg_ref, pl_ref, act, f"head_layers={head_layers} {settings}")[0])
         m.close()
     assert np.array_equal(outs[0].logits, outs[2].logits) and np.array_equal(outs[0].pooled, outs[2].pooled)
+
+
+def test_encoder_hidden_positions_past_max_pos(small_model):
+    """The padded layout gives every position a RoPE angle, so encoder_hidden refuses a len past
+    max_position_embeddings (a Batch error naming it), while forward, which runs the real tokens
+    only, serves the same batch; a token id past the vocabulary is refused by both."""
+    cfg0, agent, _, _, _ = small_model
+    cfg = dict(cfg0, max_position_embeddings=64, num_hidden_layers=2)
+    st = synth_checkpoint(json.dumps(cfg), json.dumps(agent), 5, 256, 2, True)
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent))
+    n, L = 2, 80
+    ids = np.full((n, L), 1002, np.uint32)
+    ids[:, :10] = np.arange(5, 15, dtype=np.uint32)
+    am = np.zeros((n, L), np.uint32)
+    am[:, :10] = 1
+    b = Batch(n, L, 1, ids.reshape(-1), am.reshape(-1), np.array([10, 10], np.uint64), np.array([3, 4], np.uint32),
+              np.array([1, 1], np.uint64), np.array([0, 0], np.uint32))
+    out = m.forward(b)
+    assert np.all(np.isfinite(out.logits)) and np.all(np.isfinite(out.pooled))
+    with pytest.raises(S1Error, match="max_position_embeddings"):
+        m.encoder_hidden(b)
+    bad = Batch(n, 12, 1, np.full(n * 12, 5000, np.uint32), np.ones(n * 12, np.uint32), np.array([12, 12], np.uint64),
+                np.array([3, 4], np.uint32), np.array([1, 1], np.uint64), np.array([0, 0], np.uint32))
+    for call in (m.forward, m.encoder_hidden):
+        with pytest.raises(S1Error, match="vocabulary"):
+            call(bad)
+    m.close()
 
 
 def test_very_short_rows(small_model):
