@@ -41,7 +41,9 @@ typedef struct s1_model s1_model;
  * S1_ERR_CONFIG (Knobs::parse, lib.rs:155-259). NULL or "" selects the defaults. `dtype=f16`
  * keeps weights and activations in f16, the checkpoints' own type (BackendOptions::f32 = false,
  * backend.rs:25-27, keeps the checkpoint's f16 weights); the default `dtype=bf16` rounds them to
- * bf16. Accumulation, LayerNorm, softmax and the residual stream are f32 either way. */
+ * bf16. Accumulation, LayerNorm, softmax and the residual stream are f32 either way. `dtype=f32`
+ * is BackendOptions::f32 = true: f32 weights and compute on plain f32 kernels (no fused kernels,
+ * a numerics mode, not the serving path). */
 int s1_model_create(const char* safetensors_path, const char* encoder_config_json,
                     const char* agent_config_json, const char* settings, int device_ordinal,
                     s1_model** out);
@@ -106,7 +108,8 @@ int s1_encoder_hidden(s1_model* m, uint32_t n, uint32_t len, uint32_t kmax,
  * holds it, else to a multiple of `pad=`. */
 size_t s1_padded_len(const s1_model* m, size_t len, size_t rows);
 
-/* Backend::name (lib.rs:1804-1812), e.g. "hip(gfx950,bf16)". Owned by the model. */
+/* Backend::name (lib.rs:1804-1812), e.g. "hip(gfx950,bf16)" ("f16", "f32" by dtype). Owned by
+ * the model. */
 const char* s1_name(const s1_model* m);
 
 /* Backend::active_kernels (lib.rs:1814-1824, contract backend.rs:111-116): comma list of the

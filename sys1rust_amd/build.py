@@ -31,8 +31,8 @@ COMMON = [
     "-I", str(ROOT / "include"),
 ]
 
-SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "model.cpp", "api.cpp", "safetensors.cpp", "synth.cpp",
-           "selfcheck.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "f32path.hip", "model.cpp", "api.cpp", "safetensors.cpp",
+           "synth.cpp", "selfcheck.cpp"]
 LIBS = ["-Wl,-rpath,/opt/rocm/lib"]
 
 

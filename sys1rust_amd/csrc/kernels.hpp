@@ -185,4 +185,37 @@ void gather_f32_launch(const float* x, const int* rows, int R, int d, float* out
 void rowdot_launch(const uint16_t* x, const float* w, const float* b, int R, int d, float* out, hipStream_t st,
                    int elem = ELEM_BF16);
 
+// ---- The dtype=f32 path (BackendOptions::f32): f32 weights and activations, plain kernels.
+
+// C[M, N] (+)= act(A[M, K] . W[N, K]^T + bias), all f32; accumulate adds to C (the residual).
+struct Gemm32Args {
+  const float* A = nullptr;  // [M, lda]
+  const float* W = nullptr;  // [N, ldw]
+  float* C = nullptr;        // [M, ldc]
+  const float* bias = nullptr;
+  int M = 0, N = 0, K = 0, lda = 0, ldw = 0, ldc = 0;
+  int act = ACT_NONE;
+  bool accumulate = false;
+};
+// Null when the shape is supported (K a multiple of 16, 16-byte aligned rows), else a message.
+const char* gemm32_check(const Gemm32Args& g);
+void gemm32_launch(const Gemm32Args& g, hipStream_t st);
+// qkv [T, 3d] -> q, k, v [d / 64, T, 64] f32, q and k rotated at pos[t] when cos_t is given.
+void split32_launch(const float* qkv, int T, int d, const int* pos, const float* cos_t, const float* sin_t, float* q,
+                    float* k, float* v, hipStream_t st);
+// Attention of n single queries, each over its key set: entries of 8 int32 as attn_fallback_launch
+// takes them ({query, a0, a1, b0, b1, lo, hi, zeros}); q, k, v [heads, T, 64] f32, out [T, ldo].
+struct Attn32Args {
+  const float* q = nullptr;
+  const float* k = nullptr;
+  const float* v = nullptr;
+  float* out = nullptr;
+  const int* entries = nullptr;
+  int n = 0, heads = 0, T = 0, ldo = 0;
+  float scale = 0.125f;
+};
+void attn32_launch(const Attn32Args& a, hipStream_t st);
+// act[t, i] = gelu(x[t, i]) * x[t, I + i] (exact erf) over x [T, 2I] f32.
+void geglu32_launch(const float* x, int T, int I, float* act, hipStream_t st);
+
 }  // namespace s1

@@ -114,7 +114,11 @@ Settings Settings::parse(const std::string& spec) {
     else if (key == "fusegeglu") s.fusegeglu = flag();
     else if (key == "fuseln") s.fuseln = flag();
     else if (key == "graphs") s.graphs = flag();
-    else if (key == "dtype") s.f16 = one_of({"bf16", "f16"}) == "f16";
+    else if (key == "dtype") {
+      const std::string t = one_of({"bf16", "f16", "f32"});
+      s.f16 = t == "f16";
+      s.f32 = t == "f32";
+    }
     else fail(kConfig, "hip settings: unknown setting `" + key + "` in `" + spec + "`");
     if (j == spec.size()) break;
   }
@@ -163,6 +167,10 @@ void Model::init(const SafeTensors& st, const std::string& enc_json, const std::
   // headprune prunes the last head layer; with no head layers the scorer reads the encoder's
   // stream whole, as head_forward's loop then leaves it (lib.rs:1726-1765).
   if (cfg.head_layers == 0) set.headprune = false;
+  // dtype=f32 runs the plain f32 kernels: no fused kernels, and the head's last layer over every
+  // row (headprune skips only rows nobody reads, so the outputs are the same). fuserope keeps its
+  // other meaning there: with `band` it chooses the banded local attention (lib.rs:330-361).
+  if (set.f32) set.fusegeglu = set.fuseln = set.headprune = false;
   elem = set.f16 ? ELEM_F16 : ELEM_BF16;
   // The forwards `warm` runs at load (warm_buckets) are checked before any device work.
   if (std::any_of(set.warm.begin(), set.warm.end(), [](size_t n) { return n > 0; }))
@@ -305,7 +313,7 @@ void Model::init(const SafeTensors& st, const std::string& enc_json, const std::
   if (!check_fault.empty() && check_fault != "fuserope" && check_fault != "fusegeglu" && check_fault != "fuseln")
     fail(kConfig, "SYS1HIP_CHECK_FAULT=" + check_fault + " is not one of fuserope, fusegeglu, fuseln");
   auto decide = [&](bool& on, const char* nm, const char* instead, auto&& check) {
-    if (!on) return;
+    if (!on || set.f32) return;  // the f32 path runs none of the fused kernels
     const std::string why = check(check_fault == nm);
     if (why.empty()) return;
     on = false;
@@ -328,7 +336,7 @@ void Model::init(const SafeTensors& st, const std::string& enc_json, const std::
     int64_t n = 1;
     for (auto s : it.shape) n *= s;
     offs.push_back(total);
-    total += align256(size_t(n) * (it.bf16 ? 2 : 4));
+    total += align256(size_t(n) * (it.bf16 && !set.f32 ? 2 : 4));
   }
   hip_check(hipMalloc(&wmem, total), "hipMalloc(weights)");
   char* base = static_cast<char*>(wmem);
@@ -337,7 +345,7 @@ void Model::init(const SafeTensors& st, const std::string& enc_json, const std::
     const Item& it = items[k];
     void* dptr = base + offs[k];
     *it.dst = dptr;
-    if (!it.bf16) {
+    if (!it.bf16 || set.f32) {
       std::vector<float> f = st.to_f32(it.name, it.shape);
       hip_check(hipMemcpy(dptr, f.data(), f.size() * 4, hipMemcpyHostToDevice), "upload weight");
       continue;
@@ -368,12 +376,12 @@ void Model::init(const SafeTensors& st, const std::string& enc_json, const std::
   }
 
   char nb[64];
-  std::snprintf(nb, sizeof nb, "hip(gfx950,%s)", set.f16 ? "f16" : "bf16");
+  std::snprintf(nb, sizeof nb, "hip(gfx950,%s)", set.f32 ? "f32" : set.f16 ? "f16" : "bf16");
   name = nb;
   // Backend::active_kernels (backend.rs:111-116): the custom kernels requested, built and checked
   // at this load.
   auto listed = [&](bool on, const char* k) {
-    if (on) kernels += std::string(kernels.empty() ? "" : ",") + k;
+    if (on && !set.f32) kernels += std::string(kernels.empty() ? "" : ",") + k;
   };
   listed(set.fuserope, "fuserope");
   listed(set.fusegeglu, "fusegeglu");
@@ -395,13 +403,14 @@ void Model::teardown() {
   if (wmem) (void)hipFree(wmem);
   if (rmem) (void)hipFree(rmem);
   if (amem) (void)hipFree(amem);
+  if (fmem) (void)hipFree(fmem);
   if (dmeta) (void)hipFree(dmeta);
   if (hmeta) (void)hipHostFree(hmeta);
   if (hout) (void)hipHostFree(hout);
   if (stream) (void)hipStreamDestroy(stream);
   pending.clear();
   event_pool.clear();
-  wmem = rmem = amem = nullptr;
+  wmem = rmem = amem = fmem = nullptr;
   dmeta = nullptr;
   hmeta = hout = nullptr;
   stream = nullptr;
@@ -431,10 +440,11 @@ void Model::release() {
   hip_check(hipStreamSynchronize(stream), "sync");
   drop_graphs();
   if (amem) hip_check(hipFree(amem), "hipFree(arena)");
+  if (fmem) hip_check(hipFree(fmem), "hipFree(arena)");
   if (dmeta) hip_check(hipFree(dmeta), "hipFree(meta)");
-  amem = nullptr;
+  amem = fmem = nullptr;
   dmeta = nullptr;
-  acap = dmeta_cap = 0;
+  acap = fcap = dmeta_cap = 0;
 }
 
 size_t Model::padded_len(size_t len) const {
@@ -564,6 +574,23 @@ Plan Model::plan(uint32_t n, uint32_t len, uint32_t kmax, const uint32_t* ids, c
   p.off_pooled = m.size();
   for (uint32_t r = 0; r < n; ++r) m.push_back(set.headprune ? int(r) * per : p.row_start[r]);
   pad4();
+  if (set.f32) {
+    // Every token's keys: its row (global layers), the row within the window (local layers).
+    const int W = cfg.window();
+    auto entries = [&](bool local) {
+      for (uint32_t r = 0; r < n; ++r) {
+        const int rs = p.row_start[r], re = p.row_start[r + 1];
+        for (int t = rs; t < re; ++t) {
+          const int e[8] = {t, local ? std::max(rs, t - W) : rs, local ? std::min(re, t + W + 1) : re, rs, rs, 0, 0, 0};
+          m.insert(m.end(), e, e + 8);
+        }
+      }
+    };
+    p.off_eg = m.size();
+    entries(false);
+    p.off_el = m.size();
+    entries(true);
+  }
   return p;
 }
 
@@ -658,6 +685,29 @@ Plan Model::plan_padded(uint32_t n, uint32_t len, const uint32_t* ids, const uin
   p.off_far = m.size();
   m.insert(m.end(), far.begin(), far.end());
   p.nfar = int(far.size() / 8);
+  if (set.f32) {
+    // Every position's keys in one table per layer kind: the real keys (global), the real keys
+    // of the window or, past lqend, the far entry above (local).
+    p.off_eg = m.size();
+    for (uint32_t r = 0; r < n; ++r)
+      for (int t = p.row_start[r]; t < p.row_start[r + 1]; ++t) {
+        const int e[8] = {t, p.row_start[r], kend[r], p.row_start[r], p.row_start[r], 0, 0, 0};
+        m.insert(m.end(), e, e + 8);
+      }
+    p.off_el = m.size();
+    size_t fi = 0;
+    for (uint32_t r = 0; r < n; ++r)
+      for (int t = p.row_start[r]; t < p.row_start[r + 1]; ++t) {
+        if (t < lqend[r]) {
+          const int e[8] = {t, std::max(p.row_start[r], t - W), std::min(kend[r], t + W + 1), p.row_start[r],
+                            p.row_start[r], 0, 0, 0};
+          m.insert(m.end(), e, e + 8);
+        } else {
+          m.insert(m.end(), far.begin() + fi, far.begin() + fi + 8);
+          fi += 8;
+        }
+      }
+  }
   p.off_scorer = p.off_pooled = m.size();
   return p;
 }
@@ -1226,6 +1276,10 @@ void Model::enqueue_forward(const Plan& p, const Acts& a) {
 
 void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
   if (p.n == 0) return;
+  if (set.f32) {
+    forward32(p, logits_out, pooled_out);
+    return;
+  }
   const auto t0 = std::chrono::steady_clock::now();
   hip_check(hipSetDevice(device), "hipSetDevice");
   upload(p);
@@ -1259,6 +1313,10 @@ void Model::forward(const Plan& p, float* logits_out, float* pooled_out) {
 void Model::encoder_hidden(const Plan& p, float* hidden) {
   if (p.n == 0) return;
   if (!p.padded) fail(kBackend, "encoder_hidden: the plan is not the padded layout");
+  if (set.f32) {
+    encoder_hidden32(p, hidden);
+    return;
+  }
   hip_check(hipSetDevice(device), "hipSetDevice");
   upload(p);
   Acts a = arena(p);
@@ -1271,6 +1329,203 @@ void Model::encoder_hidden(const Plan& p, float* hidden) {
     });
   });
   // The padded layout's rows are the [n, len] positions in order: [T, d] is [n, len, d].
+  hip_check(hipMemcpyAsync(hidden, a.enc, size_t(T) * d * 4, hipMemcpyDeviceToHost, stream), "download hidden");
+  hip_check(hipStreamSynchronize(stream), "encoder_hidden");
+  if (set.ops) collect_stats();
+  if (set.layers) layer_report();
+  if (set.clear) release();
+}
+
+// ---- dtype=f32 (BackendOptions::f32, backend.rs:25-27): the same graph with f32 weights and
+// activations on the plain f32 kernels, eagerly enqueued (no graphs, no fused kernels, the
+// head's last layer over every row). Every attention query reads its key set from the plan's
+// entry tables.
+
+struct Model::Acts32 {
+  float *h, *x, *qkv, *q, *k, *v, *att, *mid, *act, *enc, *hh, *sx, *s1, *logits, *pooled;
+};
+
+Model::Acts32 Model::arena32(const Plan& p) {
+  const size_t T = size_t(p.T), R = size_t(p.R), n = size_t(p.n);
+  const size_t d = size_t(cfg.d), I = size_t(cfg.inter), S = size_t(scorer_width);
+  const size_t sizes[] = {T * d, T * d, T * 3 * d, T * d, T * d, T * d, T * d, T * std::max(2 * I, 4 * d), T * I,
+                          T * d, T * d, R * d, R * S, R, n * d};
+  constexpr int NS = sizeof(sizes) / sizeof(sizes[0]);
+  size_t off[NS], total = 0;
+  for (int i = 0; i < NS; ++i) {
+    off[i] = total;
+    total += align256(std::max<size_t>(sizes[i] * 4, 16));
+  }
+  if (total > fcap) {
+    if (fmem) {
+      hip_check(hipStreamSynchronize(stream), "sync");
+      hip_check(hipFree(fmem), "hipFree(arena)");
+      fmem = nullptr;
+    }
+    const size_t cap = std::max(total, fcap * 3 / 2);
+    hip_check(hipMalloc(&fmem, cap), "hipMalloc(activations)");
+    fcap = cap;
+  }
+  float* b[NS];
+  for (int i = 0; i < NS; ++i) b[i] = reinterpret_cast<float*>(static_cast<char*>(fmem) + off[i]);
+  return Acts32{b[0], b[1], b[2], b[3], b[4], b[5], b[6], b[7], b[8], b[9], b[10], b[11], b[12], b[13], b[14]};
+}
+
+namespace {
+
+// C (+)= act(A . W^T + bias) on the f32 GEMM, shapes checked first.
+void gemm32(const float* A, int lda, const float* W, int ldw, float* C, int ldc, const float* bias, int M, int N, int K,
+            int act, bool accumulate, hipStream_t st) {
+  Gemm32Args g;
+  g.A = A;
+  g.W = W;
+  g.C = C;
+  g.bias = bias;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = lda;
+  g.ldw = ldw;
+  g.ldc = ldc;
+  g.act = act;
+  g.accumulate = accumulate;
+  if (const char* e = gemm32_check(g)) fail(kBackend, e);
+  gemm32_launch(g, st);
+}
+
+}  // namespace
+
+// encode (lib.rs:1525-1693) in f32 over the plan's rows; a.h holds the residual stream after it.
+void Model::run_encoder32(const Plan& p, const Acts32& a) {
+  const int T = p.T, d = cfg.d, I = cfg.inter, H = cfg.heads;
+  const float eps = float(cfg.eps);
+  const int* ids = dmeta + p.off_ids;
+  const int* pos = dmeta + p.off_pos;
+  // h = LN(tok_emb[ids]) (lib.rs:1534-1551)
+  op("embed", [&] {
+    gather_f32_launch(w32(tok_emb), ids, T, d, a.x, stream);
+    layernorm_launch(a.x, nullptr, emb_norm, nullptr, eps, T, d, nullptr, a.h, nullptr, nullptr, nullptr, stream, elem);
+  });
+  for (int l = 0; l < cfg.layers; ++l) {
+    const LayerWeights& L = layers[l];
+    const int tw = L.local ? 1 : 0;
+    const float* xin = a.h;  // layer 0 attends from the embedding itself
+    if (l > 0) {
+      op("attn_norm", [&] {
+        layernorm_launch(a.h, nullptr, L.attn_norm, nullptr, eps, T, d, nullptr, a.x, nullptr, nullptr, nullptr, stream,
+                         elem);
+      });
+      xin = a.x;
+    }
+    op("wqkv", [&] { gemm32(xin, d, w32(L.wqkv), d, a.qkv, 3 * d, nullptr, T, 3 * d, d, ACT_NONE, false, stream); });
+    op("split_rope", [&] { split32_launch(a.qkv, T, d, pos, rope_cos[tw], rope_sin[tw], a.q, a.k, a.v, stream); });
+    op(L.local ? "attn_local" : "attn_global", [&] {
+      Attn32Args at;
+      at.q = a.q;
+      at.k = a.k;
+      at.v = a.v;
+      at.out = a.att;
+      at.entries = dmeta + (L.local ? p.off_el : p.off_eg);
+      at.n = T;
+      at.heads = H;
+      at.T = T;
+      at.ldo = d;
+      at.scale = 1.0f / std::sqrt(float(cfg.head_dim()));
+      attn32_launch(at, stream);
+    });
+    op("wo", [&] { gemm32(a.att, d, w32(L.wo), d, a.h, d, nullptr, T, d, d, ACT_NONE, true, stream); });
+    op("mlp_norm", [&] {
+      layernorm_launch(a.h, nullptr, L.mlp_norm, nullptr, eps, T, d, nullptr, a.x, nullptr, nullptr, nullptr, stream, elem);
+    });
+    op("wi", [&] { gemm32(a.x, d, w32(L.wi), d, a.mid, 2 * I, nullptr, T, 2 * I, d, ACT_NONE, false, stream); });
+    op("geglu", [&] { geglu32_launch(a.mid, T, I, a.act, stream); });
+    op("wo2", [&] { gemm32(a.act, I, w32(L.wo2), I, a.h, d, nullptr, T, d, I, ACT_NONE, true, stream); });
+    layer_mark();
+  }
+}
+
+void Model::forward32(const Plan& p, float* logits_out, float* pooled_out) {
+  const auto t0 = std::chrono::steady_clock::now();
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  upload(p);
+  Acts32 a = arena32(p);
+  const int T = p.T, d = cfg.d, R = p.R, n = p.n, S = scorer_width;
+  const int Hh = cfg.head_nheads();
+  const float hscale = 1.0f / std::sqrt(float(d / Hh));  // head_scale (lib.rs:576-578)
+  layer_mark();
+  run_encoder32(p, a);
+  // final_norm, then the head stream hh = enc + type_emb[qtype] (lib.rs:1689, 1700-1703)
+  op("final_norm", [&] {
+    layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, type_emb, dmeta + p.off_seg,
+                     a.hh, stream, elem);
+  });
+  // head_forward (lib.rs:1698-1765): pre-norm layers with biases, ReLU FFN, every row
+  for (int j = 0; j < cfg.head_layers; ++j) {
+    const HeadWeights& Hw = head[j];
+    op("head_norm1", [&] {
+      layernorm_launch(a.hh, nullptr, Hw.n1w, Hw.n1b, 1e-5f, T, d, nullptr, a.x, nullptr, nullptr, nullptr, stream, elem);
+    });
+    op("head_in_proj", [&] { gemm32(a.x, d, w32(Hw.in_w), d, a.qkv, 3 * d, Hw.in_b, T, 3 * d, d, ACT_NONE, false, stream); });
+    op("head_split", [&] { split32_launch(a.qkv, T, d, nullptr, nullptr, nullptr, a.q, a.k, a.v, stream); });
+    op("head_attn", [&] {
+      Attn32Args at;
+      at.q = a.q;
+      at.k = a.k;
+      at.v = a.v;
+      at.out = a.att;
+      at.entries = dmeta + p.off_eg;
+      at.n = T;
+      at.heads = Hh;
+      at.T = T;
+      at.ldo = d;
+      at.scale = hscale;
+      attn32_launch(at, stream);
+    });
+    op("head_out_proj", [&] { gemm32(a.att, d, w32(Hw.out_w), d, a.hh, d, Hw.out_b, T, d, d, ACT_NONE, true, stream); });
+    op("head_norm2", [&] {
+      layernorm_launch(a.hh, nullptr, Hw.n2w, Hw.n2b, 1e-5f, T, d, nullptr, a.x, nullptr, nullptr, nullptr, stream, elem);
+    });
+    op("head_linear1",
+       [&] { gemm32(a.x, d, w32(Hw.l1_w), d, a.mid, 4 * d, Hw.l1_b, T, 4 * d, d, ACT_RELU, false, stream); });
+    op("head_linear2",
+       [&] { gemm32(a.mid, 4 * d, w32(Hw.l2_w), 4 * d, a.hh, d, Hw.l2_b, T, d, 4 * d, ACT_NONE, true, stream); });
+  }
+  // score (lib.rs:1768-1800): LayerNorm with bias at the marker rows, scorer1 + exact GELU,
+  // scorer3; pooled = position 0 of each row
+  if (R > 0) {
+    op("scorer_norm", [&] {
+      layernorm_launch(a.hh, dmeta + p.off_scorer, sc0_w, sc0_b, 1e-5f, R, d, nullptr, a.sx, nullptr, nullptr, nullptr,
+                       stream, elem);
+    });
+    op("scorer1", [&] { gemm32(a.sx, d, w32(sc1_w), d, a.s1, S, sc1_b, R, S, d, ACT_GELU, false, stream); });
+    op("scorer3", [&] { gemm32(a.s1, S, sc3_w, S, a.logits, 1, sc3_b, R, 1, S, ACT_NONE, false, stream); });
+  }
+  op("pooled", [&] { gather_f32_launch(a.hh, dmeta + p.off_pooled, n, d, a.pooled, stream); });
+  hip_check(hipGetLastError(), "kernel launch");
+  if (R > 0) hip_check(hipMemcpyAsync(logits_out, a.logits, size_t(R) * 4, hipMemcpyDeviceToHost, stream), "download logits");
+  hip_check(hipMemcpyAsync(pooled_out, a.pooled, size_t(n) * d * 4, hipMemcpyDeviceToHost, stream), "download pooled");
+  hip_check(hipStreamSynchronize(stream), "forward");
+  if (set.ops) collect_stats();
+  if (set.layers) layer_report();
+  if (set.trace) {
+    const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    std::fprintf(stderr, "forward n=%d len=%d T=%d us=%.1f\n", p.n, p.len, p.T, us);
+  }
+  if (set.clear) release();
+}
+
+void Model::encoder_hidden32(const Plan& p, float* hidden) {
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  upload(p);
+  Acts32 a = arena32(p);
+  const int T = p.T, d = cfg.d;
+  layer_mark();
+  run_encoder32(p, a);
+  op("final_norm", [&] {
+    layernorm_launch(a.h, nullptr, final_norm, nullptr, float(cfg.eps), T, d, nullptr, a.enc, nullptr, nullptr, nullptr,
+                     stream, elem);
+  });
+  hip_check(hipGetLastError(), "kernel launch");
   hip_check(hipMemcpyAsync(hidden, a.enc, size_t(T) * d * 4, hipMemcpyDeviceToHost, stream), "download hidden");
   hip_check(hipStreamSynchronize(stream), "encoder_hidden");
   if (set.ops) collect_stats();

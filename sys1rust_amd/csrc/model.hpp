@@ -48,6 +48,7 @@ struct Settings {
   bool fuseln = true;      // a split-K Wo / Wo2 finishes in the kernel of the LayerNorm after it
   bool graphs = true;      // replay each repeated batch shape from a captured HIP graph
   bool f16 = false;        // dtype=f16: weights and activations in f16 (the checkpoint's type), not bf16
+  bool f32 = false;        // dtype=f32: f32 weights and compute (BackendOptions::f32), the plain f32 kernels
   static Settings parse(const std::string& spec);
 };
 
@@ -107,6 +108,9 @@ struct Plan {
   bool padded = false;
   size_t off_far = 0;
   int nfar = 0;
+  // dtype=f32: every query's key set in attn32_launch's entry format, for global (off_eg) and
+  // local (off_el) layers, T entries each.
+  size_t off_eg = 0, off_el = 0;
 };
 
 struct Model {
@@ -138,6 +142,9 @@ struct Model {
   // activation arena, grown on demand
   void* amem = nullptr;
   size_t acap = 0;
+  // the dtype=f32 path's activation arena
+  void* fmem = nullptr;
+  size_t fcap = 0;
   // pinned host staging
   void* hmeta = nullptr;
   size_t hmeta_cap = 0;
@@ -185,6 +192,13 @@ struct Model {
 
  private:
   struct Acts;
+  struct Acts32;
+  Acts32 arena32(const Plan& p);
+  void run_encoder32(const Plan& p, const Acts32& a);
+  void forward32(const Plan& p, float* logits, float* pooled);
+  void encoder_hidden32(const Plan& p, float* hidden);
+  // The f32 GEMM weights: with dtype=f32 the 16-bit weight pointers hold f32 tensors.
+  static const float* w32(const uint16_t* w) { return reinterpret_cast<const float*>(w); }
   void init(const SafeTensors& st, const std::string& enc_json, const std::string& agent_json,
             const std::string& settings);
   void teardown();

@@ -64,15 +64,18 @@ pub fn check_settings(spec: &str) -> Result<()> {
     check(unsafe { s1_check_settings(s.as_ptr()) })
 }
 
-/// The settings libsys1hip gets: the caller's, after `dtype=f16`. laya-mlx keeps the
-/// checkpoint's f16 weights unless `BackendOptions::f32` (backend.rs:25-27); `dtype=f16` is that
-/// choice here (weights and activations in f16, f32 accumulation). The library's own default is
-/// bf16, and the caller's settings come later, so a `dtype=` of theirs wins (last mention wins).
-fn library_settings(spec: &str) -> String {
-    if spec.is_empty() {
-        "dtype=f16".to_string()
-    } else {
-        format!("dtype=f16,{spec}")
+/// The settings libsys1hip gets. laya-mlx keeps the checkpoint's f16 weights unless
+/// `BackendOptions::f32` (backend.rs:25-27): `dtype=f16` is that choice here (weights and
+/// activations in f16, f32 accumulation), put before the caller's settings so that a `dtype=` of
+/// theirs wins (last mention wins; the library's own default is bf16). With `f32` the
+/// transformer runs in f32 (`dtype=f32`, after the caller's settings: the option wins, as it
+/// does in laya-mlx).
+fn library_settings(spec: &str, f32: bool) -> String {
+    match (spec.is_empty(), f32) {
+        (true, false) => "dtype=f16".to_string(),
+        (false, false) => format!("dtype=f16,{spec}"),
+        (true, true) => "dtype=f32".to_string(),
+        (false, true) => format!("{spec},dtype=f32"),
     }
 }
 
@@ -156,14 +159,7 @@ impl HipBackend {
                     .into(),
             ));
         }
-        if opts.f32 {
-            return Err(Error::Config(
-                "laya-hip computes in f16 or bf16 with f32 accumulation; BackendOptions::f32 \
-                 (an f32 transformer) is not supported by this backend"
-                    .into(),
-            ));
-        }
-        let settings = c_string(library_settings(&opts.settings()), "settings")?;
+        let settings = c_string(library_settings(&opts.settings(), opts.f32), "settings")?;
         let enc = c_string(encoder_json(cfg), "encoder config")?;
         let agent = c_string(agent_json(cfg), "agent config")?;
 
@@ -334,9 +330,15 @@ mod tests {
 
     #[test]
     fn dtype_f16_comes_first_so_the_callers_dtype_wins() {
-        assert_eq!(library_settings(""), "dtype=f16");
-        assert_eq!(library_settings("headprune"), "dtype=f16,headprune");
-        assert_eq!(library_settings("dtype=bf16"), "dtype=f16,dtype=bf16");
+        assert_eq!(library_settings("", false), "dtype=f16");
+        assert_eq!(library_settings("headprune", false), "dtype=f16,headprune");
+        assert_eq!(library_settings("dtype=bf16", false), "dtype=f16,dtype=bf16");
+    }
+
+    #[test]
+    fn the_f32_option_comes_last_so_it_wins() {
+        assert_eq!(library_settings("", true), "dtype=f32");
+        assert_eq!(library_settings("headprune,dtype=bf16", true), "headprune,dtype=bf16,dtype=f32");
     }
 
     #[test]
@@ -347,7 +349,7 @@ mod tests {
     }
 
     #[test]
-    fn device_cpu_and_f32_are_config_errors() {
+    fn device_cpu_is_a_config_error() {
         // Checked before any weight is touched, so no checkpoint is needed: an empty
         // safetensors image (8-byte header length + "{}") stands in.
         let dir = std::env::temp_dir().join(format!("laya-hip-test-{}", std::process::id()));
@@ -364,13 +366,9 @@ mod tests {
             agent: serde_json::from_value(serde_json::json!({"encoder": "x"})).unwrap(),
             encoder: laya_core::EncoderConfig::from_value(&enc).unwrap(),
         };
-        for opts in [
-            BackendOptions { device: Device::Cpu, ..Default::default() },
-            BackendOptions { f32: true, ..Default::default() },
-        ] {
-            let e = HipBackend::new(&w, &cfg, &opts).err().unwrap();
-            assert!(matches!(e, Error::Config(_)), "{e}");
-        }
+        let opts = BackendOptions { device: Device::Cpu, ..Default::default() };
+        let e = HipBackend::new(&w, &cfg, &opts).err().unwrap();
+        assert!(matches!(e, Error::Config(_)), "{e}");
         std::fs::remove_dir_all(&dir).ok();
     }
 }

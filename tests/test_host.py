@@ -66,7 +66,7 @@ def small_ckpt():
     ("pad=x", "is not a whole number"),
     ("buckets", "needs a value"),
     ("nax=1", "`1` is not one of 0, all"),
-    ("dtype=fp8", "`fp8` is not one of bf16, f16"),
+    ("dtype=fp8", "`fp8` is not one of bf16, f16, f32"),
     ("dtype", "needs a value"),
     # warm's load-time forwards are checked before any device memory is allocated
     ("buckets=2:64,warm=1", "warm needs buckets of at least 3 tokens"),
@@ -98,7 +98,7 @@ KNOBS_KEYS = ["geglu=shapeless", "geglu=compiled", "geglu=plain", "addmm", "addm
               "buckets=512:128:256", "pad=8", "warm=1:4", "cache=512", "wired=2048", "dense_upto=1024", "headprune",
               "unpad", "fuserope", "band=512", "band=0", "nax=all", "nax=0", "directload", "sharehead",
               "parallel_load", "parallel_load=0"]
-OWN_KEYS = ["fusegeglu=0", "fuseln=0", "graphs=0", "dtype=f16", "dtype=bf16"]
+OWN_KEYS = ["fusegeglu=0", "fuseln=0", "graphs=0", "dtype=f16", "dtype=bf16", "dtype=f32"]
 
 
 @pytest.mark.parametrize("spec", KNOBS_KEYS + OWN_KEYS + [
@@ -183,7 +183,7 @@ def test_per_tensor_create_checks_the_views(small_ckpt):
     assert rc == _lib.S1_ERR_WEIGHTS and "encoder.final_norm.weight" in L.s1_last_error().decode()
 
 
-@pytest.mark.parametrize("spec", ["dtype=f16", "dtype=bf16", "dtype=f16,dtype=bf16"])
+@pytest.mark.parametrize("spec", ["dtype=f16", "dtype=bf16", "dtype=f16,dtype=bf16", "dtype=bf16,dtype=f32"])
 def test_dtype_setting_is_accepted(small_ckpt, spec):
     """A valid dtype passes the settings check: without a GPU the create fails later, at the
     device (a Backend error), never as a Config error."""
@@ -192,7 +192,7 @@ def test_dtype_setting_is_accepted(small_ckpt, spec):
     except S1Error as e:
         assert e.kind != "Config", str(e)
         return
-    want = "f16" if spec.endswith("f16") else "bf16"
+    want = spec.rsplit("=", 1)[1]
     assert m.name() == f"hip(gfx950,{want})"
     m.close()
 

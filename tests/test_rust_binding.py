@@ -135,6 +135,7 @@ def test_lib_uses_only_declared_functions_and_exports_laya_mlx_names():
     assert DEFAULT_TUNING in lib
 
 
-@pytest.mark.parametrize("needle", ["Device::Cpu", "opts.f32", "w.view()?", "s1_model_create_from_tensors"])
-def test_lib_refuses_cpu_and_f32_and_binds_through_the_view(needle):
+@pytest.mark.parametrize("needle", ["Device::Cpu", "library_settings(&opts.settings(), opts.f32)", "\"dtype=f32\"",
+                                    "w.view()?", "s1_model_create_from_tensors"])
+def test_lib_refuses_cpu_maps_f32_and_binds_through_the_view(needle):
     assert needle in (CRATE / "src" / "lib.rs").read_text()
