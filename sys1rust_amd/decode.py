@@ -73,9 +73,12 @@ def softmax_f32(z) -> np.ndarray:
 
 def act_features(logits_row, marker_count: int) -> np.ndarray:
     """decode.rs:250-259: [top1, top1 - top2, normalised entropy, k / 255] of the softmax over the
-    whole masked logits row (masked slots hold -1e4 and weigh nothing), k = max(marker_count, 2)."""
-    p = softmax_f32(logits_row)
+    whole masked logits row (masked slots hold -1e4 and weigh nothing), k = max(marker_count, 2).
+    An empty row (kmax 0) has no probabilities: top1 = top2 = 0 and the entropy sum is -0.0."""
     k = np.float32(max(int(marker_count), 2))
+    if np.asarray(logits_row).size == 0:  # a batch without answer slots: no probabilities
+        return np.array([0.0, 0.0, -0.0, k / np.float32(255.0)], dtype=np.float32)
+    p = softmax_f32(logits_row)
     ent = np.float32(-(p * np.log(np.maximum(p, np.float32(1e-9)))).sum(dtype=np.float32) / np.log(k))
     srt = np.sort(p)[::-1]
     top1 = srt[0] if srt.size else np.float32(0)
@@ -86,6 +89,8 @@ def act_features(logits_row, marker_count: int) -> np.ndarray:
 def act_features_rows(logits, kmax: int, marker_count) -> np.ndarray:
     """act_features of every row of a [n * kmax] logits buffer at once -> [n, 4]."""
     n = len(marker_count)
+    if kmax == 0:
+        return np.stack([act_features(np.zeros(0, np.float32), c) for c in marker_count]).reshape(n, 4)
     z = np.asarray(logits, dtype=np.float32)[: n * kmax].reshape(n, kmax)
     e = np.exp(z - z.max(axis=1, keepdims=True)).astype(np.float32)
     p = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)

@@ -385,6 +385,26 @@ def test_act_features_invariants():
     # top2 is the second largest, whatever the order
     f = act_features(np.log(np.array([0.2, 0.5, 0.3], np.float32)), 3)
     np.testing.assert_allclose(f[:2], [0.5, 0.2], rtol=1e-5)
+    # an empty row (a batch with kmax 0): the softmax of nothing has no top entries
+    # (unwrap_or(0.0)), its entropy sum is 0 negated, and k = max(0, 2)
+    f = act_features(np.zeros(0, np.float32), 0)
+    np.testing.assert_array_equal(f, np.array([0.0, 0.0, -0.0, 2.0 / 255.0], np.float32))
+    assert np.signbit(f[2])
+
+
+def test_act_features_rows_match_one_row_at_a_time():
+    """act_features_rows (the decode's batched form) equals act_features row by row, with and
+    without answer slots."""
+    from sys1rust_amd.decode import act_features_rows
+
+    rng = np.random.default_rng(2)
+    for kmax, counts in [(4, [4, 2, 1, 0]), (0, [0, 0])]:
+        lg = rng.normal(size=len(counts) * kmax).astype(np.float32)
+        for r, c in enumerate(counts):
+            lg[r * kmax + c: (r + 1) * kmax] = -1e4
+        got = act_features_rows(lg, kmax, counts)
+        want = np.stack([act_features(lg[r * kmax:(r + 1) * kmax], c) for r, c in enumerate(counts)])
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
 
 
 def test_act_head_matches_torch_mlp():
