@@ -134,3 +134,26 @@ def test_f32_modernbert_large_512_tokens():
     say(f"f32 large padded 600: hidden rel at every position {rel:.2e}")
     assert rel <= HIDDEN_REL_F32, rel
     m.close()
+
+
+def test_f32_mmbert_golden_batch():
+    """The mmBERT-base shape (hidden 768, 12 heads, GeGLU 1152) on its golden fixture's batch,
+    against the oracle and against transformers' hidden states."""
+    z = np.load(GOLDEN / "golden_mmbert.npz")
+    cfg = json.loads(str(z["encoder_config"]))
+    agent = json.loads(str(z["agent_config"]))
+    st = synth_checkpoint(json.dumps(cfg), json.dumps(agent), int(z["seed"]), int(z["scorer_width"]), 2, True)
+    b = Batch(int(z["n"]), int(z["len"]), int(z["kmax"]), z["input_ids"], z["attention_mask"], z["seq_lens"],
+              z["marker_pos"], z["marker_count"], z["qtype"])
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f32")
+    o = O.Oracle(st, cfg, agent)
+    ref = o.encoder_hidden(b)
+    lg, pl = o.forward(b, ref)
+    gate_f32(m, b, ref, lg, pl, ActHead.from_weights(o.w), "f32 mmbert golden")
+    hid = m.encoder_hidden(b).reshape(b.n, b.len, -1)
+    sel = z["hidden_sel"]
+    g = hid[sel[:, 0], sel[:, 1]]
+    gr = float((np.linalg.norm(g - z["hidden"], axis=-1) / np.linalg.norm(z["hidden"], axis=-1)).max())
+    say(f"f32 mmbert golden: hidden rel vs transformers {gr:.2e}")
+    assert gr <= 1e-4, gr
+    m.close()
