@@ -138,7 +138,7 @@ def test_f32_modernbert_large_512_tokens():
 
 def test_f32_mmbert_golden_batch():
     """The mmBERT-base shape (hidden 768, 12 heads, GeGLU 1152) on its golden fixture's batch,
-    against the oracle and against transformers' hidden states."""
+    against the oracle at every position, padding included."""
     z = np.load(GOLDEN / "golden_mmbert.npz")
     cfg = json.loads(str(z["encoder_config"]))
     agent = json.loads(str(z["agent_config"]))
@@ -150,10 +150,29 @@ def test_f32_mmbert_golden_batch():
     ref = o.encoder_hidden(b)
     lg, pl = o.forward(b, ref)
     gate_f32(m, b, ref, lg, pl, ActHead.from_weights(o.w), "f32 mmbert golden")
+    m.close()
+
+
+@pytest.mark.parametrize("case", ["golden_small", "golden_large", "golden_mmbert"])
+def test_f32_against_the_independent_fixtures(case):
+    """The f32 option straight against the golden fixtures written by transformers'
+    ModernBertModel (hidden states) and torch's TransformerEncoderLayer head and scorer (logits,
+    pooled rows), at the tolerances the oracle itself meets against them."""
+    z = np.load(GOLDEN / f"{case}.npz")
+    cfg = json.loads(str(z["encoder_config"]))
+    agent = json.loads(str(z["agent_config"]))
+    st = synth_checkpoint(json.dumps(cfg), json.dumps(agent), int(z["seed"]), int(z["scorer_width"]), 2, True)
+    b = Batch(int(z["n"]), int(z["len"]), int(z["kmax"]), z["input_ids"], z["attention_mask"], z["seq_lens"],
+              z["marker_pos"], z["marker_count"], z["qtype"])
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f32")
     hid = m.encoder_hidden(b).reshape(b.n, b.len, -1)
     sel = z["hidden_sel"]
     g = hid[sel[:, 0], sel[:, 1]]
-    gr = float((np.linalg.norm(g - z["hidden"], axis=-1) / np.linalg.norm(z["hidden"], axis=-1)).max())
-    say(f"f32 mmbert golden: hidden rel vs transformers {gr:.2e}")
-    assert gr <= 1e-4, gr
+    rel = float((np.linalg.norm(g - z["hidden"], axis=-1) / np.linalg.norm(z["hidden"], axis=-1)).max())
+    out = m.forward(b)
+    dl = float(np.abs(out.logits - z["logits"]).max())
+    pg, pr = out.pooled.reshape(b.n, -1), z["pooled"].reshape(b.n, -1)
+    dp = float((np.linalg.norm(pg - pr, axis=-1) / np.linalg.norm(pr, axis=-1)).max())
+    say(f"f32 {case} against the fixture: hidden rel {rel:.2e}, logits {dl:.2e}, pooled rel {dp:.2e}")
+    assert rel < 1e-4 and dl < 1e-5 and dp < 1e-4, (rel, dl, dp)
     m.close()
