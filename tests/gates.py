@@ -158,3 +158,24 @@ def gate_model(m, b, ref_hidden, ref_logits, ref_pooled, act, tag, rows=None, pr
     say(f"{tag}: pooled rel {prel:.3e}")
     assert prel <= HIDDEN_REL_GATE, (tag, prel)
     return out, summary
+
+
+def random_batch(rng, vocab: int, pad_id: int) -> Batch:
+    """A right-padded batch of 1-9 rows of 1-300 tokens, up to 6 answer slots, markers at distinct
+    real tokens of their row (any count up to kmax, 0 included), random question types."""
+    n = int(rng.integers(1, 10))
+    lens = rng.integers(1, 301, size=n)
+    L = int(lens.max()) + int(rng.integers(0, 20))
+    kmax = int(rng.integers(0, 7))
+    ids = rng.integers(5, vocab - 24, size=(n, L)).astype(np.uint32)
+    am = np.zeros((n, L), np.uint32)
+    mp = np.zeros((n, kmax), np.uint32)
+    mc = np.zeros(n, np.uint64)
+    for r, ln in enumerate(lens):
+        am[r, :ln] = 1
+        ids[r, ln:] = pad_id
+        k = int(rng.integers(0, min(kmax, ln) + 1))
+        mc[r] = k
+        mp[r, :k] = np.sort(rng.choice(ln, size=k, replace=False))
+    return Batch(n, L, kmax, ids.reshape(-1), am.reshape(-1), lens.astype(np.uint64), mp.reshape(-1), mc,
+                 rng.integers(0, 3, size=n).astype(np.uint32))

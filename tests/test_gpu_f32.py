@@ -21,7 +21,7 @@ from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
 from sys1rust_amd.decode import ActHead, decode_answers
 from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, Batch, workload
 
-from gates import hidden_rel, say
+from gates import decisive_checkpoint, hidden_rel, random_batch, say
 
 pytestmark = pytest.mark.gpu
 
@@ -175,4 +175,21 @@ def test_f32_against_the_independent_fixtures(case):
     dp = float((np.linalg.norm(pg - pr, axis=-1) / np.linalg.norm(pr, axis=-1)).max())
     say(f"f32 {case} against the fixture: hidden rel {rel:.2e}, logits {dl:.2e}, pooled rel {dp:.2e}")
     assert rel < 1e-4 and dl < 1e-5 and dp < 1e-4, (rel, dl, dp)
+    m.close()
+
+
+def test_f32_random_batches(small):
+    """Six of the seeded random batches (ragged rows of 1-300 tokens, 0-6 answer slots) on the
+    decisive-scorer checkpoint, every position of encoder_hidden included."""
+    cfg, agent, st, _ = small
+    st = decisive_checkpoint(st)
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings="dtype=f32")
+    o = O.Oracle(st, cfg, agent)
+    act = ActHead.from_weights(o.w)
+    rng = np.random.default_rng(20261202)
+    for case in range(6):
+        b = random_batch(rng, cfg["vocab_size"], cfg["pad_token_id"])
+        ref = o.encoder_hidden(b)
+        lg, pl = o.forward(b, ref)
+        gate_f32(m, b, ref, lg, pl, act, f"f32 random {case} n={b.n} len={b.len} kmax={b.kmax}")
     m.close()

@@ -26,7 +26,8 @@ from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, S1Error, synth_chec
 from sys1rust_amd.decode import ActHead
 from sys1rust_amd.workloads import AGENT, MODERNBERT_LARGE, Batch, workload
 
-from gates import HIDDEN_REL_GATE, FUSED, check_answers, gate_model, hidden_rel, say
+from gates import (HIDDEN_REL_GATE, FUSED, check_answers, decisive_checkpoint, gate_model, hidden_rel,
+                   random_batch, say)
 
 pytestmark = pytest.mark.gpu
 
@@ -338,6 +339,28 @@ def test_row_subsets_after_other_batches_match_oracle(small_model, settings):
         prel = float(np.linalg.norm(out.pooled - pl_ref) / np.linalg.norm(pl_ref))
         say(f"rows {rows}: pooled rel {prel:.3e}")
         assert prel <= HIDDEN_REL_GATE, (rows, prel)
+
+
+@pytest.mark.parametrize("settings", ["", DEFAULT_TUNING])
+def test_random_batches_match_oracle(small_model, settings):
+    """Twelve seeded random batches (ragged rows of 1-300 tokens, so one to three 128-query local
+    tiles and one or two 256-query global tiles per row and head, 0-6 answer slots, markers
+    anywhere in the row) through encoder_hidden and forward, each against the oracle with every
+    gate, on the decisive-scorer checkpoint."""
+    cfg, agent, st, _, _ = small_model
+    st = decisive_checkpoint(st)
+    m = HipBackend(st, json.dumps(cfg), json.dumps(agent), settings=settings)
+    o = O.Oracle(st, cfg, agent)
+    act = ActHead.from_weights(o.w)
+    rng = np.random.default_rng(20261202)
+    for case in range(12):
+        b = random_batch(rng, cfg["vocab_size"], cfg["pad_token_id"])
+        tag = f"random {case} ({settings[:12]!r}) n={b.n} len={b.len} kmax={b.kmax} T={b.total_tokens()}"
+        say(tag)
+        ref = o.encoder_hidden(b)
+        lg, pl = o.forward(b, ref)
+        gate_model(m, b, ref, lg, pl, act, tag)
+    m.close()
 
 
 def _reencode(st: bytes, dtype: str) -> bytes:
