@@ -407,6 +407,39 @@ def test_act_features_rows_match_one_row_at_a_time():
         np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
 
 
+def test_decode_batch_matches_one_row_at_a_time():
+    """decode_answers over a batch (the [n, kmax] array form from VECTOR_ROWS rows on) gives what
+    each row decoded alone gives (the loop over rows): rows are independent. Random logits at
+    three scales, exact ties, rows with 0 and 1 options, every question type, clamped and
+    per-bucket temperatures."""
+    from sys1rust_amd.decode import VECTOR_ROWS, decode_answers
+
+    rng = np.random.default_rng(3)
+    for trial in range(300):
+        n = int(rng.integers(VECTOR_ROWS, 12))
+        kmax = int(rng.integers(1, 14))
+        mc = rng.integers(0, kmax + 1, size=n).astype(np.uint64)
+        qt = rng.integers(0, 3, size=n).astype(np.uint32)
+        lg = (rng.standard_normal(n * kmax) * [0.01, 1.0, 30.0][trial % 3]).astype(np.float32)
+        if trial % 7 == 0:
+            lg[:] = np.float32(0.5)  # every option tied: the first one wins
+        for r in range(n):
+            lg[r * kmax + int(mc[r]): (r + 1) * kmax] = np.float32(-1e4)
+        temps = [(1.0, 1.0, 1.0), (0.7, 2.0, "3"), (True, None, float("nan"))][trial % 3]
+        tbo = {"choice:3-5": 0.9, "noul:2": 4.0} if trial % 5 == 0 else None
+        batch = decode_answers(lg, kmax, mc, qt, temps, tbo)
+        for r in range(n):
+            one = decode_answers(lg[r * kmax:(r + 1) * kmax], kmax, mc[r:r + 1], qt[r:r + 1], temps, tbo)[0]
+            x = batch[r]
+            assert x.keys() == one.keys() and x["type"] == one["type"]
+            np.testing.assert_allclose(x["probabilities"], one["probabilities"], rtol=1e-12, atol=1e-15)
+            for key in x:
+                if key == "choice":
+                    assert x[key] == one[key], (trial, r, x, one)
+                elif key not in ("type", "probabilities"):
+                    assert abs(x[key] - one[key]) <= 1e-12, (trial, r, key, x[key], one[key])
+
+
 def test_act_head_matches_torch_mlp():
     """ActHead.probs (decode.rs:226-246) against torch's Linear -> GELU -> Linear -> softmax, an
     independent implementation, on the synthetic checkpoint's act_head; a head of zeros gives the
