@@ -50,10 +50,9 @@ LOGITS_ABS_GATE = 0.15  # laya-mlx/tests/parity.rs:33-37, logits_max_abs < 0.15
 
 
 def _decision(y) -> int:
-    p = y["probabilities"]
-    if y["type"] == "noul":
-        return int(p[1] >= 0.5)
-    return int(np.argmax(p))
+    if y["type"] == "noul":  # noul = p[1], or 0 for a question with fewer than two options
+        return int(y["noul"] >= 0.5)
+    return int(np.argmax(y["probabilities"]))
 
 
 def check_answers(lg_gpu, lg_ref, b: Batch, tag: str, prob_gate: float | None = PROB_ABS_GATE):

@@ -21,7 +21,7 @@ from sys1rust_amd.backend import DEFAULT_TUNING, HipBackend, synth_checkpoint
 from sys1rust_amd.decode import ActHead
 from sys1rust_amd.workloads import MMBERT_BASE, Batch, workload
 
-from gates import FUSED, HIDDEN_REL_GATE, gate_model, hidden_rel, say
+from gates import FUSED, HIDDEN_REL_GATE, gate_model, hidden_rel, random_batch, say
 
 pytestmark = pytest.mark.gpu
 
@@ -73,6 +73,20 @@ def test_mmbert_base_requests_every_row(mmbert, name):
     ref = o.encoder_hidden(b)
     lg, pl = o.forward(b, ref)
     gate_model(m, b, ref, lg, pl, act, f"mmbert {name}")
+
+
+def test_mmbert_random_batches(mmbert):
+    """Four seeded random batches (1-9 ragged rows of 1-300 tokens, 0-6 answer slots) at this
+    shape, whose 128-token local window is the widest the staged local kernel takes."""
+    m, o, st, act = mmbert
+    rng = np.random.default_rng(768)
+    for case in range(4):
+        b = random_batch(rng, MMBERT_BASE["vocab_size"], MMBERT_BASE["pad_token_id"])
+        tag = f"mmbert random {case}: n={b.n} len={b.len} kmax={b.kmax} T={b.total_tokens()}"
+        say(tag)
+        ref = o.encoder_hidden(b)
+        lg, pl = o.forward(b, ref)
+        gate_model(m, b, ref, lg, pl, act, tag)
 
 
 def test_mmbert_base_f16(mmbert):

@@ -341,7 +341,7 @@ def test_row_subsets_after_other_batches_match_oracle(small_model, settings):
         assert prel <= HIDDEN_REL_GATE, (rows, prel)
 
 
-@pytest.mark.parametrize("settings", ["", DEFAULT_TUNING])
+@pytest.mark.parametrize("settings", ["", DEFAULT_TUNING, "dtype=f16"])
 def test_random_batches_match_oracle(small_model, settings):
     """Twelve seeded random batches (ragged rows of 1-300 tokens, so one to three 128-query local
     tiles and one or two 256-query global tiles per row and head, 0-6 answer slots, markers

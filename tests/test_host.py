@@ -486,3 +486,16 @@ def test_geglu_gemm_refuses_a_bias(entry):
     rc = getattr(L, entry)(buf, K, buf, K, buf, N // 2, bias, M, N, K, 2, 0, None)
     assert rc == _lib.S1_ERR_CONFIG, L.s1_last_error()
     assert "GeGLU epilogue takes no bias" in L.s1_last_error().decode()
+
+
+def test_answer_gate_takes_questions_with_one_option():
+    """The parity gate's decisions (tests/gates.py) read the decode's own fields: a noul question
+    with a single option has noul 0 (decode.rs) and no second probability to read."""
+    from gates import check_answers
+    from sys1rust_amd.workloads import Batch
+
+    lg = np.array([0.3, -1e4, 1.5, -0.2, 0.7, -1e4], np.float32)
+    b = Batch(3, 4, 2, np.zeros(12, np.uint32), np.ones(12, np.uint32), np.full(3, 4, np.uint64),
+              np.array([1, 0, 1, 2, 3, 0], np.uint32), np.array([1, 2, 1], np.uint64), np.array([2, 2, 0], np.uint32))
+    summary = check_answers(lg, lg, b, "one-option rows")
+    assert summary["rows"] == 3 and summary["waived"] == 0 and summary["max_dp"] == 0.0
