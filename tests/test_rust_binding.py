@@ -135,6 +135,45 @@ def test_lib_uses_only_declared_functions_and_exports_laya_mlx_names():
     assert DEFAULT_TUNING in lib
 
 
+def _call_args(text: str, start: int) -> list[str]:
+    """The top-level comma-separated arguments of the call whose '(' is at text[start]."""
+    depth, cur, args = 0, [], []
+    for ch in text[start:]:
+        if ch in "([{":
+            depth += 1
+            if depth == 1:
+                continue
+        elif ch in ")]}":
+            depth -= 1
+            if depth == 0:
+                break
+        if depth == 1 and ch == ",":
+            args.append("".join(cur).strip())
+            cur = []
+        else:
+            cur.append(ch)
+    last = "".join(cur).strip()
+    if last:
+        args.append(last)
+    return args
+
+
+def test_lib_calls_pass_the_declared_argument_counts():
+    """Every call of a C function in src/lib.rs passes as many arguments as src/ffi.rs declares
+    (and the header takes), counted at the top level of the call's parentheses."""
+    decl = rust_functions()
+    lib = (CRATE / "src" / "lib.rs").read_text()
+    calls = 0
+    for m in re.finditer(r"\b(s1_\w+)\s*\(", lib):
+        name = m.group(1)
+        if lib[max(0, m.start() - 7): m.start()].endswith("fn "):
+            continue  # a definition, not a call
+        args = _call_args(lib, m.end() - 1)
+        assert len(args) == len(decl[name][1]), (name, args, decl[name][1])
+        calls += 1
+    assert calls >= 10, calls
+
+
 @pytest.mark.parametrize("needle", ["Device::Cpu", "library_settings(&opts.settings(), opts.f32)", "\"dtype=f32\"",
                                     "w.view()?", "s1_model_create_from_tensors"])
 def test_lib_refuses_cpu_maps_f32_and_binds_through_the_view(needle):
