@@ -21,6 +21,7 @@ host's cores, whole requests of each shape: the median of repeated timings after
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -249,24 +250,32 @@ def main() -> int:
     def run(b, steps, warmup, model=model):
         """`steps` requests after `warmup`: the forward (batch upload, GPU work, outputs back) and
         the CPU answer decode with the action head. Returns the mean ms per request over the timed
-        region, the op statistics, and the per-request forward and decode times (ms)."""
+        region, the op statistics, and the per-request forward and decode times (ms). Python's
+        garbage collector is paused over the timed steps (collected just before), as timeit does,
+        so that a collection of the interpreter's heap does not land inside one request."""
         for _ in range(warmup):
             out = model.forward(b)
             decode_answers(out.logits, b.kmax, b.marker_count, b.qtype, pooled=out.pooled, act_head=act)
         model.op_stats_reset()
         fwd, dec = [], []
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for _ in range(steps):
-            t0 = time.perf_counter()
-            out = model.forward(b)
-            t1 = time.perf_counter()
-            decode_answers(out.logits, b.kmax, b.marker_count, b.qtype, pooled=out.pooled, act_head=act)
-            t2 = time.perf_counter()
-            fwd.append((t1 - t0) * 1e3)
-            dec.append((t2 - t1) * 1e3)
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t) * 1e3 / steps, model.op_stats(), fwd, dec
+        gc.collect()
+        gc.disable()
+        try:
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(steps):
+                t0 = time.perf_counter()
+                out = model.forward(b)
+                t1 = time.perf_counter()
+                decode_answers(out.logits, b.kmax, b.marker_count, b.qtype, pooled=out.pooled, act_head=act)
+                t2 = time.perf_counter()
+                fwd.append((t1 - t0) * 1e3)
+                dec.append((t2 - t1) * 1e3)
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t
+        finally:
+            gc.enable()
+        return elapsed * 1e3 / steps, model.op_stats(), fwd, dec
 
     def shape_line(ms, fwd, dec) -> dict:
         tot = [a + c for a, c in zip(fwd, dec)]
