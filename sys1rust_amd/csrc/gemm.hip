@@ -7,9 +7,12 @@
 //
 // Tiling: a BM x BN x 64 block tile in 4 wavefronts; each wave owns a (BM/WM) x (BN/WN) sub-tile
 // computed with v_mfma_f32_32x32x16_bf16 (v_mfma_f32_32x32x16_f16 for f16 operands: the element
-// type E is a template parameter). Operands move global -> LDS directly (global_load_lds_dwordx4,
-// no registers), STAGES k-tiles deep, one barrier per k-tile; a 16-byte-chunk XOR swizzle keeps
-// the fragment reads free of bank conflicts.
+// type E is a template parameter). Operands move global -> LDS directly (buffer_load_dwordx4 with
+// lds, no registers), STAGES k-tiles deep, one barrier per k-tile; a 16-byte-chunk XOR swizzle
+// keeps the fragment reads free of bank conflicts. The addresses the k-loop needs are computed
+// before it: per lane, a 32-bit offset per direct load (a k-tile adds one scalar offset) and a
+// base per k-step and operand (a fragment adds an immediate), so the loop issues almost nothing
+// but its loads, LDS reads and MFMAs.
 //
 // MFMA 32x32x16 lane layout (per operand, lane l, h = l / 32): the first operand supplies row
 // l % 32, k = 8h..8h+7; the second supplies column l % 32, k = 8h..8h+7; the 16 accumulators of
@@ -29,6 +32,14 @@
 
 #include "device.hpp"
 #include "kernels.hpp"
+
+// buffer_load_dwordx4 ... lds: a direct global -> LDS load (LDS address from M0, lane l at + 16 l)
+// whose global address is a buffer resource (scalar) plus a per-lane 32-bit offset and a scalar
+// offset; offsets past the resource's size read 0. The LLVM intrinsic behind it is bound by name,
+// outside any namespace so that the declaration keeps external linkage.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ void raw_buffer_load_lds(i32x4 rsrc, __attribute__((address_space(3))) void* lds, int size, int voffset,
+                                    int soffset, int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 
 namespace s1 {
 
@@ -55,6 +66,22 @@ __device__ __forceinline__ uint4 lds_load16_a8(const char* p) {
 // The "memory" clobber keeps LDS accesses on their side of it; completion of the async loads is
 // awaited explicitly with wait_vmcnt before it.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_barrier" ::: "memory"); }
+
+// Raw buffer resource over [p, p + bytes): base address, no stride, the byte count, and the third
+// dword of every gfx9 buffer resource (32-bit data format, no swizzle).
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xffff));
+  r.z = __builtin_amdgcn_readfirstlane(int(bytes));
+  r.w = 0x00020000;
+  return r;
+}
+
+// Bytes from the start of a [rows, ld] 16-bit matrix to the end of its k columns (gemm_check keeps
+// it below 4 GiB, so a 32-bit offset reaches every element).
+__host__ __device__ inline size_t span_bytes(int rows, int ld, int k) { return (size_t(rows - 1) * ld + k) * 2; }
 
 // Wait until at most `ahead` k-tiles of this wave's loads (LPW loads each) are in flight.
 template <int LPW, int MAXA>
@@ -111,27 +138,36 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
-  // Global -> LDS without registers (global_load_lds_dwordx4): lane l of a load moves 16 bytes
-  // of row l / CH of its RG-row group, chunk (l % CH) ^ swizzle, into slot l % CH.
+  // Global -> LDS without registers: lane l of a load moves 16 bytes of row l / CH of its RG-row
+  // group, chunk (l % CH) ^ swizzle, into slot l % CH. Load group gi (A groups first) fills KiB gi
+  // of its stage; the wave's load j is group wave + j NW, which reads A exactly when j < AG / NW.
+  static_assert(AG % NW == 0 && A_BYTES == AG * 1024, "a wave's j-th load reads one operand, into KiB gi");
   const int lrow = lane / CH, lslot = lane % CH;
+  // Per-lane byte offset of each of this wave's loads from the start of its operand at k = 0.
+  uint32_t voff[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int gi = wave + j * NW;
+    const bool isA = j < AG / NW;
+    const int r = (isA ? gi : gi - AG) * RG + lrow;
+    const int c = lslot ^ ((r / SW) % CH);
+    voff[j] = isA ? uint32_t((size_t(min(m0 + r, g.M - 1)) * g.lda + c * 8) * 2)
+                  : uint32_t((size_t(n0 + r) * g.ldw + c * 8) * 2);
+  }
+  const i32x4 rsrcA = buffer_rsrc(g.A, uint32_t(span_bytes(g.M, g.lda, g.K)));
+  const i32x4 rsrcW = buffer_rsrc(g.W, uint32_t(span_bytes(g.N, g.ldw, g.K)));
   // Loads j in [jlo, jhi) of this wave's LPW for k-tile kt into stage `stage`.
-  auto issue = [&](int stage, int kt, int jlo, int jhi) {
-    char* sb = smem + stage * STAGE_BYTES;
+  auto issue = [&](int stage, int kt, int jlo, int jhi) __attribute__((always_inline)) {
+    const int koff = __builtin_amdgcn_readfirstlane(kt * BK * 2);
+    char* sb = smem + stage * STAGE_BYTES + wave * 1024;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       if (j < jlo || j >= jhi) continue;
-      const int gi = wave + j * NW;
-      if (gi < AG) {
-        const int r = gi * RG + lrow;
-        const int c = lslot ^ ((r / SW) % CH);
-        const uint16_t* src = g.A + size_t(min(m0 + r, g.M - 1)) * g.lda + kt * BK + c * 8;
-        __builtin_amdgcn_global_load_lds(src, sb + gi * 1024, 16, 0, 0);
-      } else {
-        const int r = (gi - AG) * RG + lrow;
-        const int c = lslot ^ ((r / SW) % CH);
-        const uint16_t* src = g.W + size_t(n0 + r) * g.ldw + kt * BK + c * 8;
-        __builtin_amdgcn_global_load_lds(src, sb + A_BYTES + (gi - AG) * 1024, 16, 0, 0);
-      }
+      const bool isA = j < AG / NW;
+      raw_buffer_load_lds(isA ? rsrcA : rsrcW,
+                          reinterpret_cast<__attribute__((address_space(3))) void*>(
+                              uint32_t(reinterpret_cast<uintptr_t>(sb + j * NW * 1024))),
+                          16, int(voff[j]), koff, 0, 0);
     }
   };
 
@@ -148,6 +184,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
     if (s < NK) issue(s, kt0 + s, 0, LPW);
 
   const int lr = lane & 31, lh = lane >> 5;
+  // Fragment reads: lane (lr, lh) of k-step ks reads A row wm TM + 32 i + lr and W row
+  // wn TN + 32 j + lr, chunk (2 ks + lh) ^ ((row / SW) % CH). A row base 32 i + (multiple of 16)
+  // leaves the swizzle to the lane alone (SW CH = 16), so each k-step has one LDS base per operand
+  // and a fragment adds 32 i ROWB (an immediate) to it.
+  static_assert(SW * CH == 16 && TM % 16 == 0 && TN % 16 == 0, "lane-only fragment swizzle");
+  constexpr int KS = BK / 16;
+  int kA[KS], kW[KS];
+  {
+    const int lsw = lh ^ ((lr / SW) % CH);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int part = lr * ROWB + (((ks * 2) ^ lsw) << 4);
+      kA[ks] = wm * TM * ROWB + part;
+      kW[ks] = A_BYTES + wn * TN * ROWB + part;
+    }
+  }
   for (int it = 0; it < NK; ++it) {
     // This wave's loads of k-tile `it` are done once at most `ahead` later k-tiles are in flight.
     wait_ahead<LPW, STAGES - 2>(min(STAGES - 2, NK - 1 - it));
@@ -160,23 +212,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
     const bool pre = it + STAGES - 1 < NK;
     const int pstage = (it + STAGES - 1) % STAGES, pkt = kt0 + it + STAGES - 1;
     const char* sa = smem + (it % STAGES) * STAGE_BYTES;
-    const char* sw = sa + A_BYTES;
     typedef typename E::v8 v8;
     v8 af[2][FM], bw[2][FN];
-    auto frag = [&](int ks, int buf) {
+    auto frag = [&](int ks, int buf) __attribute__((always_inline)) {
+      const char* pa = sa + kA[ks];
+      const char* pw = sa + kW[ks];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = wm * TM + i * 32 + lr;
-        af[buf][i] = *reinterpret_cast<const v8*>(sa + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
-      }
+      for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const v8*>(pa + i * 32 * ROWB);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int row = wn * TN + j * 32 + lr;
-        bw[buf][j] = *reinterpret_cast<const v8*>(sw + row * ROWB + (((ks * 2 + lh) ^ ((row / SW) % CH)) << 4));
-      }
+      for (int j = 0; j < FN; ++j) bw[buf][j] = *reinterpret_cast<const v8*>(pw + j * 32 * ROWB);
     };
     frag(0, 0);
-    constexpr int KS = BK / 16, LPK = (LPW + 1) / 2;
+    constexpr int LPK = (LPW + 1) / 2;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (pre && ks < 2) issue(pstage, pkt, ks * LPK, min(LPW, (ks + 1) * LPK));
@@ -762,6 +809,9 @@ const char* gemm_check(const GemmArgs& g) {
   if (g.K <= 0 || g.K % BK) return "gemm: K must be a positive multiple of 64";
   if (g.N <= 0 || g.N % 128) return "gemm: N must be a positive multiple of 128";
   if (g.lda < g.K || g.ldw < g.K || (g.lda % 8) || (g.ldw % 8)) return "gemm: bad leading dimension";
+  // The direct loads address each operand by a 32-bit byte offset from its start.
+  if (span_bytes(g.M, g.lda, g.K) >= (size_t(1) << 32) || span_bytes(g.N, g.ldw, g.K) >= (size_t(1) << 32))
+    return "gemm: A and W must each span less than 4 GiB";
   if (g.epi == EPI_ROPE && (g.rope_d % 64 || g.N != 3 * g.rope_d)) return "gemm: rope epilogue needs N = 3d, d % 64 == 0";
   if (g.epi == EPI_ROPE && (g.rope_ldv % 8 || g.rope_ldv < g.M + 64)) return "gemm: v row stride must be a multiple of 8 and >= M + 64";
   if (g.splits < 1 || g.splits > g.K / BK) return "gemm: splits must be in 1..K/64";
