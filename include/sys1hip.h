@@ -160,8 +160,9 @@ void s1_op_stats_reset(s1_model* m);
 
 /* C = A[M,K] . W[N,K]^T. epi 0: C bf16 (+bias, act 0 none / 1 relu / 2 gelu); 1: C f32 += acc
  * (+bias); 2: GeGLU on W with rows interleaved by 32 (x, gate), C bf16 [M, N/2];
- * 3: C f32 = acc (+bias). K a multiple of 64, N of 128; A and W each span less than 4 GiB
- * ((rows - 1) ld + K elements), else S1_ERR_CONFIG before anything reaches the GPU. */
+ * 3: C f32 = acc (+bias). K a multiple of 64, N of 128; W spans less than 4 GiB ((N - 1) ldw
+ * + K elements), and an A that spans more runs as row pieces (8 rows of it must span less),
+ * else S1_ERR_CONFIG before anything reaches the GPU. */
 int s1k_gemm(const void* A, int lda, const void* W, int ldw, void* C, int ldc, const float* bias,
              int M, int N, int K, int epi, int act, void* stream);
 

@@ -79,9 +79,11 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
   return r;
 }
 
-// Bytes from the start of a [rows, ld] 16-bit matrix to the end of its k columns (gemm_check keeps
-// it below 4 GiB, so a 32-bit offset reaches every element).
+// Bytes from the start of a [rows, ld] 16-bit matrix to the end of its k columns. Every launch
+// keeps both operands' spans below 4 GiB (W by gemm_check; A by gemm_launch, which runs a longer
+// A as row pieces), so a 32-bit offset reaches every element.
 __host__ __device__ inline size_t span_bytes(int rows, int ld, int k) { return (size_t(rows - 1) * ld + k) * 2; }
+constexpr size_t kMaxSpan = (size_t(1) << 32) - 1;
 
 // Wait until at most `ahead` k-tiles of this wave's loads (LPW loads each) are in flight.
 template <int LPW, int MAXA>
@@ -809,9 +811,11 @@ const char* gemm_check(const GemmArgs& g) {
   if (g.K <= 0 || g.K % BK) return "gemm: K must be a positive multiple of 64";
   if (g.N <= 0 || g.N % 128) return "gemm: N must be a positive multiple of 128";
   if (g.lda < g.K || g.ldw < g.K || (g.lda % 8) || (g.ldw % 8)) return "gemm: bad leading dimension";
-  // The direct loads address each operand by a 32-bit byte offset from its start.
-  if (span_bytes(g.M, g.lda, g.K) >= (size_t(1) << 32) || span_bytes(g.N, g.ldw, g.K) >= (size_t(1) << 32))
-    return "gemm: A and W must each span less than 4 GiB";
+  // The direct loads address each operand by a 32-bit byte offset from its start: W must span
+  // less than 4 GiB; a longer A runs as row pieces (unsplit only, and at least 8 rows a piece).
+  if (span_bytes(g.N, g.ldw, g.K) > kMaxSpan) return "gemm: W must span less than 4 GiB";
+  if (span_bytes(g.M, g.lda, g.K) > kMaxSpan && (g.splits > 1 || span_bytes(8, g.lda, g.K) > kMaxSpan))
+    return "gemm: an A spanning 4 GiB or more needs an unsplit product and rows under 512 MiB";
   if (g.epi == EPI_ROPE && (g.rope_d % 64 || g.N != 3 * g.rope_d)) return "gemm: rope epilogue needs N = 3d, d % 64 == 0";
   if (g.epi == EPI_ROPE && (g.rope_ldv % 8 || g.rope_ldv < g.M + 64)) return "gemm: v row stride must be a multiple of 8 and >= M + 64";
   if (g.splits < 1 || g.splits > g.K / BK) return "gemm: splits must be in 1..K/64";
@@ -832,7 +836,21 @@ const char* gemm_check(const GemmArgs& g) {
 
 void gemm_launch_partials(const GemmArgs& g, hipStream_t st) { launch_e<EPI_F32>(g, st); }
 
-void gemm_launch(const GemmArgs& g, hipStream_t st) {
+namespace {
+
+// Rows per launch for an A spanning 4 GiB or more: the fewest equal pieces, each a whole number of
+// 384 rows (a multiple of every tile height, so only the last piece has a partial tile) or of 8
+// (the q|k|v epilogue's token groups) when 384 rows already pass the limit.
+int rows_per_piece(const GemmArgs& g) {
+  const long long rmax = (long long)((kMaxSpan - size_t(g.K) * 2) / (size_t(g.lda) * 2)) + 1;
+  const long long unit = rmax >= 384 ? 384 : 8;
+  for (long long np = (g.M + rmax - 1) / rmax;; ++np) {
+    const long long r = ((g.M + np - 1) / np + unit - 1) / unit * unit;
+    if (r <= rmax) return int(r);
+  }
+}
+
+void gemm_launch_one(const GemmArgs& g, hipStream_t st) {
   if (g.splits > 1) {
     gemm_launch_partials(g, st);  // partials only: the kernel returns before its epilogue
     const long long n = (long long)g.M * (g.N / 2);
@@ -847,6 +865,34 @@ void gemm_launch(const GemmArgs& g, hipStream_t st) {
     case EPI_GEGLU: launch_e<EPI_GEGLU>(g, st); break;
     case EPI_F32: launch_e<EPI_F32>(g, st); break;
     case EPI_ROPE: launch_e<EPI_ROPE>(g, st); break;
+  }
+}
+
+}  // namespace
+
+void gemm_launch(const GemmArgs& g, hipStream_t st) {
+  if (span_bytes(g.M, g.lda, g.K) <= kMaxSpan) {
+    gemm_launch_one(g, st);
+    return;
+  }
+  // Row pieces (gemm_check allows this only unsplit): each piece is the product over its rows,
+  // launched with A, the output rows and the row positions offset to its first row.
+  const int step = rows_per_piece(g);
+  const bool f32out = g.epi == EPI_RESID || g.epi == EPI_F32;
+  for (int m0 = 0; m0 < g.M; m0 += step) {
+    GemmArgs p = g;
+    p.M = std::min(step, g.M - m0);
+    p.A = g.A + size_t(m0) * g.lda;
+    if (g.epi == EPI_ROPE) {
+      // q and k are [H, rope_T, 64] (rope_T, the head stride, stays), v is [H, 64, rope_ldv].
+      p.rope_q = g.rope_q + size_t(m0) * 64;
+      p.rope_k = g.rope_k + size_t(m0) * 64;
+      p.rope_v = g.rope_v + m0;
+      if (g.rope_pos) p.rope_pos = g.rope_pos + m0;
+    } else {
+      p.C = static_cast<char*>(g.C) + size_t(m0) * g.ldc * (f32out ? 4 : 2);
+    }
+    gemm_launch_one(p, st);
   }
 }
 

@@ -122,6 +122,44 @@ def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M, N):
     assert bool(((act - r).abs() <= r.abs() * 2 ** -7 + 1e-4).all()), float((act - r).abs().max())
 
 
+def test_gemm_a_spanning_4_gib_runs_as_row_pieces(dev):
+    """The GEMM's direct loads address A by 32-bit byte offsets from its start, so an A that
+    spans 4 GiB or more ((M - 1) lda + K 16-bit elements) runs as row pieces, each a launch of
+    its own. Here A's rows are 2 MiB apart (lda = 2^20), so 2100 rows span 4.4 GB and run as
+    pieces of 1152 and 948 rows; every epilogue must give the bits of the same product over a
+    contiguous A (lda = K), whose single launch takes the same tile configuration and k order."""
+    M, N, K, lda = 2100, 256, 256, 1 << 20
+    assert ((M - 1) * lda + K) * 2 >= 1 << 32
+    say(f"gemm over a 4 GiB A: M={M} N={N} K={K} lda={lda}")
+    L = _lib()
+    g = torch.Generator(device="cpu").manual_seed(11)
+    A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
+    W = bf16_bits(torch.randn(N, K, generator=g) * 0.05).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.1).to(dev)
+    big = torch.empty(M, lda, dtype=torch.int16, device=dev)  # 4.4 GB; only the first K columns are read
+    big[:, :K] = A
+    h0 = torch.randn(M, N, generator=g).to(dev)
+    for epi, act, b in [(0, 2, bias), (1, 0, bias), (2, 0, None), (3, 0, bias)]:
+        outs = []
+        for src, ld in [(A, K), (big, lda)]:
+            if epi == 1:
+                out = h0.clone()
+            elif epi == 3:
+                out = torch.zeros(M, N, dtype=torch.float32, device=dev)
+            else:
+                out = torch.zeros(M, N // 2 if epi == 2 else N, dtype=torch.int16, device=dev)
+            L.check(L.lib().s1k_gemm(ptr(src), ld, ptr(W), K, ptr(out), out.shape[1], ptr(b) if b is not None else None,
+                                     M, N, K, epi, act, stream()))
+            torch.cuda.synchronize()
+            outs.append(out)
+        say(f"  epi={epi}: bit-identical {torch.equal(outs[0], outs[1])}")
+        assert torch.equal(outs[0], outs[1]), epi
+    ref = as_f32(A) @ as_f32(W).T + bias
+    assert float((outs[1] - ref).abs().max()) <= 2e-5 * float(ref.abs().max()) + 1e-5
+    del big
+    torch.cuda.empty_cache()
+
+
 def test_split_k_back_to_back_shapes(dev):
     """Split-K launches of other shapes and split counts in a row, each reusing the workspace
     the previous one left: every result is complete and repeats bit for bit."""

@@ -490,20 +490,29 @@ def test_geglu_gemm_refuses_a_bias(entry):
 
 @pytest.mark.parametrize("entry", ["s1k_gemm", "s1k_gemm_noalloc"])
 @pytest.mark.parametrize("which", ["A", "W"])
-def test_gemm_refuses_operands_spanning_4_gib(entry, which):
-    """The GEMM's direct loads address A and W by 32-bit byte offsets from their starts, so an
-    operand whose rows reach 4 GiB ((rows - 1) ld + K 16-bit elements) is refused with a Config
-    error before anything reaches the GPU. One k-tile (K = 64) keeps the plan unsplit, so no
-    workspace is touched; the buffers are never read."""
+def test_gemm_refuses_operands_it_cannot_address(entry, which):
+    """The GEMM's direct loads address A and W by 32-bit byte offsets from their starts. W must
+    span less than 4 GiB ((N - 1) ldw + K 16-bit elements); an A that spans more runs as row
+    pieces, which needs 8 rows to span less than 4 GiB. Either is refused with a Config error
+    before anything reaches the GPU. One k-tile (K = 64) keeps the plan unsplit, so no workspace
+    is touched; the buffers are never read."""
     L = _lib.lib()
     buf = C.create_string_buffer(64)
-    K, ld = 64, 1024
-    big = (1 << 32) // (2 * ld) + 128  # rows: (big - 1) ld + K elements pass 4 GiB; a multiple of 128
-    M, N = (big, 256) if which == "A" else (256, big)
-    assert ((big - 1) * ld + K) * 2 >= 1 << 32 and ((big - 129) * ld + K) * 2 < 1 << 32
-    rc = getattr(L, entry)(buf, ld, buf, ld, buf, N, None, M, N, K, 0, 0, None)
+    K = 64
+    if which == "W":
+        ld = 1024
+        big = (1 << 32) // (2 * ld) + 128  # (big - 1) ld + K elements pass 4 GiB; a multiple of 128
+        assert ((big - 1) * ld + K) * 2 >= 1 << 32 and ((big - 129) * ld + K) * 2 < 1 << 32
+        M, N, lda, ldw = 256, big, K, ld
+        want = "W must span less than 4 GiB"
+    else:
+        lda = 1 << 29  # 8 rows span 7 GiB
+        assert (7 * lda + K) * 2 >= 1 << 32
+        M, N, ldw = 16, 256, K
+        want = "rows under 512 MiB"
+    rc = getattr(L, entry)(buf, lda, buf, ldw, buf, N, None, M, N, K, 0, 0, None)
     assert rc == _lib.S1_ERR_CONFIG, L.s1_last_error()
-    assert "span less than 4 GiB" in L.s1_last_error().decode()
+    assert want in L.s1_last_error().decode()
 
 
 def test_answer_gate_takes_questions_with_one_option():
