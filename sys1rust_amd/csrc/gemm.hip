@@ -106,7 +106,7 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 // as one 8-byte (bf16) or 16-byte (f32) access after a packed conversion. !TR: D = A . W^T, a
 // lane holds one column and four consecutive rows per g; only the transposed v output of the
 // q|k|v epilogue ([H, 64, ldv], rows = tokens contiguous) wants that.
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR, int KG>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, bool TR, int KG, bool PIPE = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0, int n0, int kt0, int NK, int split) {
   constexpr int NW = WM * WN;                // waves; each owns a TM x TN sub-tile
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -181,64 +181,132 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < NK) issue(s, kt0 + s, 0, LPW);
-
-  const int lr = lane & 31, lh = lane >> 5;
-  // Fragment reads: lane (lr, lh) of k-step ks reads A row wm TM + 32 i + lr and W row
-  // wn TN + 32 j + lr, chunk (2 ks + lh) ^ ((row / SW) % CH). A row base 32 i + (multiple of 16)
-  // leaves the swizzle to the lane alone (SW CH = 16), so each k-step has one LDS base per operand
-  // and a fragment adds 32 i ROWB (an immediate) to it.
-  static_assert(SW * CH == 16 && TM % 16 == 0 && TN % 16 == 0, "lane-only fragment swizzle");
-  constexpr int KS = BK / 16;
-  int kA[KS], kW[KS];
-  {
-    const int lsw = lh ^ ((lr / SW) % CH);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int part = lr * ROWB + (((ks * 2) ^ lsw) << 4);
-      kA[ks] = wm * TM * ROWB + part;
-      kW[ks] = A_BYTES + wn * TN * ROWB + part;
-    }
-  }
-  for (int it = 0; it < NK; ++it) {
-    // This wave's loads of k-tile `it` are done once at most `ahead` later k-tiles are in flight.
-    wait_ahead<LPW, STAGES - 2>(min(STAGES - 2, NK - 1 - it));
-    // Every wave's loads of `it` have landed, and every wave is done with k-tile it - 1, whose
-    // buffer the next issue overwrites.
-    barrier_lds();
-    // The next k-tile's loads go out over the first two k-steps of this one: issued as one burst
-    // they fill the address queue and stall the wave before its MFMAs (the two then do not
-    // overlap); issued later they have too little of the k-tile left to land in.
-    const bool pre = it + STAGES - 1 < NK;
-    const int pstage = (it + STAGES - 1) % STAGES, pkt = kt0 + it + STAGES - 1;
-    const char* sa = smem + (it % STAGES) * STAGE_BYTES;
+  if constexpr (PIPE) {
+    // One workgroup per CU (one wave per SIMD), so no other wave hides this one's waits: four
+    // stages (three k-tiles in flight), fragments read one k-step ahead of their MFMAs into four
+    // register sets, and the barrier that publishes k-tile it + 1 placed after k-step 1 of k-tile
+    // it, so that it + 1's first two k-steps are read during it's last two. The loads of k-tile
+    // it + 3 go out in two halves, after that barrier and after k-step 2 (in one burst they fill
+    // the address queue and hold the wave before its MFMAs: Wo2 at a 10-question request 44.9
+    // against 40.9 µs). Past the last k-tile the loads repeat it, so every k-tile waits on the
+    // same vmcnt. The sched_barriers keep each k-step's MFMAs, reads and loads in this order.
+    static_assert(STAGES == 4 && BK == 64 && TR && KG == 1, "pipelined k-loop shape");
     typedef typename E::v8 v8;
-    v8 af[2][FM], bw[2][FN];
-    auto frag = [&](int ks, int buf) __attribute__((always_inline)) {
-      const char* pa = sa + kA[ks];
-      const char* pw = sa + kW[ks];
+    const int lr = lane & 31, lh = lane >> 5;
+    constexpr int KS = BK / 16;
+    int kA[KS], kW[KS];
+    {
+      const int lsw = lh ^ ((lr / SW) % CH);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const v8*>(pa + i * 32 * ROWB);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int part = lr * ROWB + (((ks * 2) ^ lsw) << 4);
+        kA[ks] = wm * TM * ROWB + part;
+        kW[ks] = A_BYTES + wn * TN * ROWB + part;
+      }
+    }
+    v8 fa[4][FM], fb[4][FN];
+    auto rd = [&](int buf, int tile, int ks) __attribute__((always_inline)) {
+      const char* st = smem + (tile & 3) * STAGE_BYTES;
+      const char* pa = st + kA[ks];
+      const char* pw = st + kW[ks];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bw[buf][j] = *reinterpret_cast<const v8*>(pw + j * 32 * ROWB);
+      for (int i = 0; i < FM; ++i) fa[buf][i] = *reinterpret_cast<const v8*>(pa + i * 32 * ROWB);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) fb[buf][j] = *reinterpret_cast<const v8*>(pw + j * 32 * ROWB);
     };
-    frag(0, 0);
-    constexpr int LPK = (LPW + 1) / 2;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (pre && ks < 2) issue(pstage, pkt, ks * LPK, min(LPW, (ks + 1) * LPK));
-      if (ks + 1 < KS) frag(ks + 1, (ks + 1) & 1);
+    auto mm = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (TR)
-            acc[i][j] = E::mfma(bw[ks & 1][j], af[ks & 1][i], acc[i][j]);
-          else
-            acc[i][j] = E::mfma(af[ks & 1][i], bw[ks & 1][j], acc[i][j]);
-        }
+        for (int j = 0; j < FN; ++j) acc[i][j] = E::mfma(fb[buf][j], fa[buf][i], acc[i][j]);
+    };
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) issue(s, kt0 + min(s, NK - 1), 0, LPW);
+    wait_vmcnt<2 * LPW>();
+    barrier_lds();
+    rd(0, 0, 0);
+    rd(1, 0, 1);
+    for (int it = 0; it < NK; ++it) {
+      mm(0);
+      rd(2, it, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(1);
+      rd(3, it, 3);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<LPW>();
+      barrier_lds();
+      issue((it + 3) & 3, kt0 + min(it + 3, NK - 1), 0, LPW / 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(2);
+      rd(0, min(it + 1, NK - 1), 0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue((it + 3) & 3, kt0 + min(it + 3, NK - 1), LPW / 2, LPW);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(3);
+      rd(1, min(it + 1, NK - 1), 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<0>();
+  } else {
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < NK) issue(s, kt0 + s, 0, LPW);
+  
+    const int lr = lane & 31, lh = lane >> 5;
+    // Fragment reads: lane (lr, lh) of k-step ks reads A row wm TM + 32 i + lr and W row
+    // wn TN + 32 j + lr, chunk (2 ks + lh) ^ ((row / SW) % CH). A row base 32 i + (multiple of 16)
+    // leaves the swizzle to the lane alone (SW CH = 16), so each k-step has one LDS base per operand
+    // and a fragment adds 32 i ROWB (an immediate) to it.
+    static_assert(SW * CH == 16 && TM % 16 == 0 && TN % 16 == 0, "lane-only fragment swizzle");
+    constexpr int KS = BK / 16;
+    int kA[KS], kW[KS];
+    {
+      const int lsw = lh ^ ((lr / SW) % CH);
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int part = lr * ROWB + (((ks * 2) ^ lsw) << 4);
+        kA[ks] = wm * TM * ROWB + part;
+        kW[ks] = A_BYTES + wn * TN * ROWB + part;
+      }
+    }
+    for (int it = 0; it < NK; ++it) {
+      // This wave's loads of k-tile `it` are done once at most `ahead` later k-tiles are in flight.
+      wait_ahead<LPW, STAGES - 2>(min(STAGES - 2, NK - 1 - it));
+      // Every wave's loads of `it` have landed, and every wave is done with k-tile it - 1, whose
+      // buffer the next issue overwrites.
+      barrier_lds();
+      // The next k-tile's loads go out over the first two k-steps of this one: issued as one burst
+      // they fill the address queue and stall the wave before its MFMAs (the two then do not
+      // overlap); issued later they have too little of the k-tile left to land in.
+      const bool pre = it + STAGES - 1 < NK;
+      const int pstage = (it + STAGES - 1) % STAGES, pkt = kt0 + it + STAGES - 1;
+      const char* sa = smem + (it % STAGES) * STAGE_BYTES;
+      typedef typename E::v8 v8;
+      v8 af[2][FM], bw[2][FN];
+      auto frag = [&](int ks, int buf) __attribute__((always_inline)) {
+        const char* pa = sa + kA[ks];
+        const char* pw = sa + kW[ks];
+  #pragma unroll
+        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const v8*>(pa + i * 32 * ROWB);
+  #pragma unroll
+        for (int j = 0; j < FN; ++j) bw[buf][j] = *reinterpret_cast<const v8*>(pw + j * 32 * ROWB);
+      };
+      frag(0, 0);
+      constexpr int LPK = (LPW + 1) / 2;
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (pre && ks < 2) issue(pstage, pkt, ks * LPK, min(LPW, (ks + 1) * LPK));
+        if (ks + 1 < KS) frag(ks + 1, (ks + 1) & 1);
+  #pragma unroll
+        for (int i = 0; i < FM; ++i)
+  #pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            if constexpr (TR)
+              acc[i][j] = E::mfma(bw[ks & 1][j], af[ks & 1][i], acc[i][j]);
+            else
+              acc[i][j] = E::mfma(af[ks & 1][i], bw[ks & 1][j], acc[i][j]);
+          }
+      }
     }
   }
 
@@ -381,7 +449,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
         constexpr int RS = NT / (BN / 4);
         constexpr int PT = HRF / RS;
         static_assert(PT * RS == HRF, "the staged rows split evenly over the threads");
-        constexpr int PG = PT > 8 ? (PT % 2 ? 1 : PT / 2) : PT;
+        constexpr int PG = PT <= 8 ? PT : PT % 8 == 0 ? 8 : PT % 6 == 0 ? 6 : PT % 4 == 0 ? 4 : PT % 2 == 0 ? 2 : 1;
         static_assert(PT % PG == 0 && PG <= 8, "piece groups");
         const int r0 = tid / (BN / 4), c4 = tid % (BN / 4);
         const int row0 = m0 + half * HRF + r0;
@@ -577,7 +645,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem0, int m0
   }
 }
 
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG, bool PIPE = false>
 __global__ __launch_bounds__(WM * WN * 64 * KG) void gemm_kernel(GemmArgs g) {
   // STAGES k-tiles of A [BM][BK] and W [BN][BK], bf16, rows of BK * 2 bytes. The 16-byte chunk c
   // of row r sits at slot c ^ ((r / SW) % CH): the 16 lanes of one LDS access phase (16
@@ -612,13 +680,13 @@ __global__ __launch_bounds__(WM * WN * 64 * KG) void gemm_kernel(GemmArgs g) {
       return;
     }
   }
-  gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, true, KG>(g, smem, m0, n0, kt0, NK, split);
+  gemm_tile<E, BM, BN, BK, STAGES, WM, WN, EPI, true, KG, PIPE>(g, smem, m0, n0, kt0, NK, split);
 }
 
-template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG = 1>
+template <class E, int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI, int KG = 1, bool PIPE = false>
 void launch_t(const GemmArgs& g, hipStream_t st) {
   const int mt = (g.M + BM - 1) / BM, nt = g.N / BN;
-  hipLaunchKernelGGL((gemm_kernel<E, BM, BN, BK, STAGES, WM, WN, EPI, KG>), dim3(mt * nt, g.splits),
+  hipLaunchKernelGGL((gemm_kernel<E, BM, BN, BK, STAGES, WM, WN, EPI, KG, PIPE>), dim3(mt * nt, g.splits),
                      dim3(WM * WN * 64 * KG), 0, st, g);
 }
 
@@ -633,30 +701,36 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
 //          tiles in 4 waves of 96 x 64, two stages (80 KiB, two per CU, the whole LDS). Per
 //          k-tile a CU moves 40 KiB for 3.1 MFLOP (128 x 128: 32 KiB for 2.1 MFLOP), and each
 //          wave's 6 MFMAs per fragment pair cover the LDS reads of the next k-step;
-//   mid    (the rest, e.g. the 1024-wide Wo / Wo2 at a 10-question request): the same 64 x 128
+//   long   (200 to 256 192 x 128 tiles and K >= 2048, e.g. Wo2 at a 10-question request): one
+//          round of 192 x 128 tiles, one workgroup per CU with the pipelined k-loop (four stages,
+//          160 KiB); Wo2 there 43.5 -> 40.9 µs against the mid tiles (bit-identical), where the
+//          1024-deep Wo runs 23.3 -> 25.0 and stays mid. Not for the q|k|v epilogue (mid);
+//   mid    (the rest, e.g. the 1024-wide Wo at a 10-question request): the same 64 x 128
 //          tiles as small, two stages (48 KiB, three per CU); three times the tiles of 192-row
 //          tiles, spread evenly over the CUs where 192-row tiles would leave some CUs idle.
 // (A tile count that reaches 700 128 x 128 tiles always reaches 400 192 x 128 tiles, so 128-row
 // tiles are not used.)
 constexpr int SMALL_M = 1024;
-enum TileCfg { TC_SMALL, TC_WIDE, TC_MID };
-inline TileCfg tile_cfg(int M, int N) {
+enum TileCfg { TC_SMALL, TC_WIDE, TC_MID, TC_LONG };
+inline TileCfg tile_cfg(int M, int N, int K) {
   if (M <= SMALL_M) return TC_SMALL;
   const long long t128 = (long long)((M + 127) / 128) * (N / 128);
   if (t128 < 200) return TC_SMALL;
   const long long t192 = (long long)((M + 191) / 192) * (N / 128);
+  if (t192 >= 200 && t192 <= 256 && K >= 2048) return TC_LONG;
   return t192 >= 400 ? TC_WIDE : TC_MID;
 }
-inline int tile_m_of(int M, int N) {
-  switch (tile_cfg(M, N)) {
+inline int tile_m_of(int M, int N, int K) {
+  switch (tile_cfg(M, N, K)) {
     case TC_WIDE: return 192;
+    case TC_LONG: return 192;
     default: return 64;
   }
 }
 
 template <class E, int EPI>
 void launch_te(const GemmArgs& g, hipStream_t st) {
-  switch (tile_cfg(g.M, g.N)) {
+  switch (tile_cfg(g.M, g.N, g.K)) {
     case TC_SMALL: {
       // Four k-tiles in flight when the launch fits one workgroup per CU (96 KiB of LDS each):
       // deeper prefetch for the weight stream. Past one workgroup per CU, 128 x 128 tiles with
@@ -686,6 +760,10 @@ void launch_te(const GemmArgs& g, hipStream_t st) {
     }
     case TC_WIDE: launch_t<E, 192, 128, 64, 2, 2, 2, EPI>(g, st); break;
     case TC_MID: launch_t<E, 64, 128, 64, 2, 2, 2, EPI>(g, st); break;
+    case TC_LONG:
+      if constexpr (EPI == EPI_ROPE) launch_t<E, 64, 128, 64, 2, 2, 2, EPI>(g, st);
+      else launch_t<E, 192, 128, 64, 4, 2, 2, EPI, 1, true>(g, st);
+      break;
   }
 }
 
@@ -788,7 +866,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g) {
 
 GemmPlan gemm_plan(int M, int N, int K, bool reduce_folded) {
   GemmPlan p;
-  const int bm = tile_m_of(M, N);
+  const int bm = tile_m_of(M, N, K);
   const int tiles = ((M + bm - 1) / bm) * (N / 128);
   const int KT = K / BK;
   // Few tiles (a short request on a narrow output): split K so that up to 256 workgroups run

@@ -122,6 +122,29 @@ def test_gemm_epilogues_bias_relu_gelu_residual_geglu(dev, M, N):
     assert bool(((act - r).abs() <= r.abs() * 2 ** -7 + 1e-4).all()), float((act - r).abs().max())
 
 
+@pytest.mark.parametrize("M", [5686, 5000])
+def test_gemm_long_k_one_round_pipelined(dev, M):
+    """One round of 192 x 128 tiles (200 to 256 of them) with K >= 2048 takes the pipelined
+    one-workgroup-per-CU k-loop: Wo2 of a 10-question request (5686 x 1024 x 2624) and a shorter
+    M ending on a partial row tile. f32, bf16 and residual outputs against a float32 product."""
+    N, K = 1024, 2624
+    say(f"long-K gemm M={M}")
+    g = torch.Generator(device="cpu").manual_seed(M)
+    A = bf16_bits(torch.randn(M, K, generator=g)).to(dev)
+    W = bf16_bits(torch.randn(N, K, generator=g) * 0.02).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.1).to(dev)
+    ref = as_f32(A) @ as_f32(W).T
+    scale = float(ref.abs().max())
+    out = gemm(A, W, M, N, K, epi=3)
+    assert float((out - ref).abs().max()) <= 2e-5 * scale + 1e-6
+    ob = as_f32(gemm(A, W, M, N, K, epi=0))
+    assert bool(((ob - ref).abs() <= ref.abs() * 2 ** -8 + 1e-5 * scale).all())
+    h0 = torch.randn(M, N, generator=g).to(dev)
+    h = h0.clone()
+    gemm(A, W, M, N, K, epi=1, bias=bias, C_out=h)
+    assert float((h - (h0 + ref + bias)).abs().max()) <= 2e-5 * scale + 1e-5
+
+
 def test_gemm_a_spanning_4_gib_runs_as_row_pieces(dev):
     """The GEMM's direct loads address A by 32-bit byte offsets from its start, so an A that
     spans 4 GiB or more ((M - 1) lda + K 16-bit elements) runs as row pieces, each a launch of
